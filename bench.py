@@ -1,0 +1,185 @@
+"""The hot path's benchmark: ferrite's block-float decode on one MI355X, on BASELINE config 3 (Llama-3.1-8B's shape,
+attention and the output layer in bfp8, every MLP matrix in bfp4, a bf16 KV cache at context 2048, batch 1).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c3-bfp8|c2] [--batch B] [--no-cpu]
+
+Prints ONE JSON line: tokens/s of the whole decode step (every kernel of it replayed as one HIP graph, inputs resident
+in HBM), the dominant GEMV's achieved HBM bandwidth against the 8 TB/s peak (timed live with HIP events on its own
+stream), each GEMV's GB/s, and the CPU baseline: the numpy restatement (oracle/) of one block and the output layer
+timed on this host's cores and scaled to a token. Synthetic data: random-init weights, drawn on the GPU and packed
+there."""
+import argparse, json, os, statistics, sys, time
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s (published)
+
+
+def config(name):
+  from ferrite_amd import llama as G
+  r = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
+  if name in ("c3", "c3-bfp8"):
+    c = G.model(dim=4096, heads=32, kv=8, layers=32, eps=1e-5, theta=500000.0, vocab=128256, ffn=14336, places=2048, rope=r)
+    return c, ("experts" if name == "c3" else "bfp8"), 2048
+  if name == "c2":
+    c = G.model(dim=576, heads=9, kv=3, layers=30, eps=1e-5, theta=10000.0, vocab=49152, ffn=1536, places=256, tied=True)
+    return c, "bfp8", 144
+  raise SystemExit(f"unknown config {name}")
+
+
+def timed_graph(fn, reps, stream):
+  """Captures fn into a HIP graph, replays it reps times between two HIP events on `stream` (the stream the kernels
+  are launched on), returns milliseconds per replay."""
+  with torch.cuda.stream(stream):
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+      fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps): g.replay()
+    b.record(stream)
+    b.synchronize()
+  return a.elapsed_time(b) / reps
+
+
+def gemv_rates(dec, stream, reps=5):
+  """Each GEMV of the step, launched back to back over every block's weight (so each launch reads a matrix the last
+  ones did not: 32 distinct matrices, past the 256 MB Infinity Cache), in a graph timed by events: (name, fmt, bytes a
+  launch, us a launch, GB/s)."""
+  from ferrite_amd import lib, ops
+  c = dec.c
+  x = torch.randn(dec.batch, max(c.dim, c.ffn, c.heads * dec.hd), device=dec.device)
+  out = {}
+  for name in ("qkv", "o", "gate_up", "down", "head"):
+    ws = [getattr(L, name) for L in dec.layers] if name != "head" else [dec.head] * 4
+    y = torch.empty(dec.batch, max(w.N for w in ws), device=dec.device)
+    def run():
+      for w in ws: ops.gemv(x[:, :w.K], w, out=y[:, :w.N])
+    ms = timed_graph(run, reps, stream)
+    per = ms / len(ws) * 1e-3
+    w = ws[0]
+    nbytes = w.nbytes + dec.batch * (w.K + w.N) * 4  # W + x + y, each read or written once
+    out[name] = dict(fmt=w.fmt, K=w.K, N=w.N, bytes=nbytes, us=per * 1e6, gbs=nbytes / per / 1e9)
+  return out
+
+
+def cpu_baseline(c, mode, context, layers_timed=1):
+  """The numpy restatement (oracle/llama.py) of one decode token on this host: one block at the step's context plus the
+  output layer, each the median of 3 timed runs after a warm-up, the block's time scaled by c.layers. Float64 caches,
+  as models/llama.py's main makes them (activations promote to float64)."""
+  from oracle import llama as OL
+  from oracle import bfp as O
+  rng = np.random.default_rng(0)
+  hd = c.dim // c.heads
+  oc = OL.model(dim=c.dim, heads=c.heads, kv=c.kv, layers=1, eps=c.eps, theta=c.theta, vocab=c.vocab, ffn=c.ffn,
+                places=context, rope=c.rope)
+  p = {"input_layernorm": np.ones((1, c.dim), np.float32), "post_attention_layernorm": np.ones((1, c.dim), np.float32)}
+  # block-float values as the GPU holds them; drawn already in float32 (the timing does not depend on the values)
+  for name, shape in (("qkv_proj", (c.dim, (c.heads + 2 * c.kv) * hd)), ("o_proj", (c.heads * hd, c.dim)),
+                      ("gate_up_proj", (c.dim, 2 * c.ffn)), ("down_proj", (c.ffn, c.dim))):
+    p[name] = rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)
+  cos, sin, t = OL.rotary(oc, context)
+  cache = np.zeros((2 * c.kv, context, hd))
+  x = rng.standard_normal((1, c.dim))
+  place = context - 1
+  mask = OL.masked([place], context)
+  tables = (cos[[place]], sin[[place]], t)
+  def block():
+    OL.layer(x, p, oc, tables, mask, cache, [place])
+  head_w = rng.standard_normal((c.dim, c.vocab), dtype=np.float32) * np.float32(0.02)
+  def head():
+    return OL.rms(x, p["input_layernorm"], oc) @ head_w
+  times = {}
+  for name, fn in (("block", block), ("head", head)):
+    fn()
+    ts = []
+    for _ in range(3):
+      t0 = time.perf_counter(); fn(); ts.append(time.perf_counter() - t0)
+    times[name] = statistics.median(ts)
+  per_token = times["block"] * c.layers + times["head"]
+  return dict(value=1.0 / per_token, unit="tokens/s", cores=len(os.sched_getaffinity(0)), kind="port",
+              sample=f"numpy oracle: 1 of {c.layers} blocks at context {context} + output layer, median of 3, block x{c.layers}; "
+                     f"float64 cache (activations float64), float32 weights",
+              block_s=times["block"], head_s=times["head"])
+
+
+def main():
+  ap = argparse.ArgumentParser()
+  ap.add_argument("--gpus", type=int, default=1)
+  ap.add_argument("--steps", type=int, default=50)
+  ap.add_argument("--warmup", type=int, default=5)
+  ap.add_argument("--config", default="c3")
+  ap.add_argument("--batch", type=int, default=1)
+  ap.add_argument("--no-cpu", action="store_true")
+  args = ap.parse_args()
+  if args.gpus != 1:
+    print("bench.py measures one GPU: this build has no multi-GPU path (the decode would shard by columns, as DESIGN.md says)",
+          file=sys.stderr)
+    raise SystemExit(2)
+  from ferrite_amd import lib
+  from ferrite_amd import llama as G
+  lib.load()
+  dev = torch.device("cuda:0")
+  c, mode, context = config(args.config)
+  t0 = time.time()
+  dec = G.Decoder(c, G.random_weights(c, seed=1, device=dev), mode=mode, kv="bf16", batch=args.batch, context=context,
+                  slots=args.batch)
+  torch.cuda.synchronize()
+  print(f"# weights packed on the GPU in {time.time() - t0:.1f}s: {dec.weight_bytes() / 1e9:.3f} GB", file=sys.stderr, flush=True)
+  for cache in dec.cache: cache.normal_(0, 1)  # a full context of keys and values
+  stream = torch.cuda.Stream(device=dev)
+  B = args.batch
+  place = context - 1
+  with torch.cuda.stream(stream):
+    dec.ids.copy_(torch.arange(B, dtype=torch.int32) * 7 + 1)
+    dec.set_rows([place] * B, list(range(B)))
+    dec.step(replay=True)  # captures the step's graph
+    for _ in range(args.warmup): dec.graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(args.steps): dec.graph.replay()
+    b.record(stream)
+    b.synchronize()
+  ms = a.elapsed_time(b) / args.steps
+  tok_s = B * 1000.0 / ms
+  kv_bytes = c.layers * 2 * c.kv * dec.hd * context * 2 * B
+  step_bytes = dec.weight_bytes() + kv_bytes
+  print(f"# step {ms:.3f} ms, {tok_s:.1f} tok/s, {step_bytes / 1e9:.3f} GB a step -> {step_bytes / ms / 1e6:.0f} GB/s", file=sys.stderr, flush=True)
+  rates = gemv_rates(dec, stream)
+  for k, r in rates.items():
+    print(f"# gemv {k:8s} {r['fmt']} {r['K']}x{r['N']}: {r['us']:.2f} us, {r['gbs']:.0f} GB/s ({r['gbs'] * 1e9 / HBM_PEAK:.1%})", file=sys.stderr, flush=True)
+  dom = max(rates, key=lambda k: rates[k]["bytes"] * (c.layers if k != "head" else 1))
+  r = rates[dom]
+  cpu = None
+  if not args.no_cpu:
+    cpu = cpu_baseline(c, mode, context)
+    print(f"# cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} cores (block {cpu['block_s']:.3f}s, head {cpu['head_s']:.3f}s)", file=sys.stderr)
+    cpu = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
+  line = {
+    "metric": "8B-shape bfp8 decode tok/s @bs1; GEMV HBM GB/s as % of peak",
+    "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+    "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+    "dtype": "bfp8/bfp4 weights, fp32 math", "data": "synthetic (random-init weights, random bf16 KV cache)",
+    "config": {"workload": f"BASELINE config 3: Llama-3.1-8B-shape decode, batch {B}, context {context}, "
+                           f"{'attention+head bfp8, MLP bfp4' if mode == 'experts' else 'all bfp8'}, bf16 KV",
+               "global_batch": B, "seq_len": context, "parallelism": "none (1 GPU)"},
+    "step_gbs": round(step_bytes / ms / 1e6, 1), "step_bytes": step_bytes,
+    "roofline": {"bound": "hbm", "kernel": f"gemv {dom} ({r['fmt']} {r['K']}x{r['N']})", "achieved": round(r["gbs"], 1),
+                 "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(r["gbs"] * 1e9 / HBM_PEAK, 4), "traffic": None},
+    "gemv_gbs": {k: round(v["gbs"], 1) for k, v in rates.items()},
+    "gemv_us": {k: round(v["us"], 3) for k, v in rates.items()},
+    "cpu_baseline": cpu,
+  }
+  print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+  main()

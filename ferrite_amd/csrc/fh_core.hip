@@ -1,0 +1,231 @@
+// Errors, block-float packing and unpacking, embedding rows and argmax: the small kernels of libferrite_hip.so.
+#include <stdarg.h>
+#include <string.h>
+#include "fh_common.h"
+
+namespace fh {
+
+static thread_local char g_error[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof g_error, fmt, ap);
+  va_end(ap);
+}
+
+int check_launch(const char* kernel) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: %s", kernel, hipGetErrorString(e));
+    return FH_EHIP;
+  }
+  return FH_OK;
+}
+
+// ---- packing: one thread a block of 16 ---------------------------------------------------------------------------
+// A block is (outer, inner): outer = the run of 16 (N/16 of them for FH_AXIS_N, K/16 for FH_AXIS_K), inner = the other
+// axis's index. Its value j sits at src[inner * s_inner + outer * s_outer + j * s_elem]; its bytes go to
+// mant[(outer * n_inner + inner) * (16 or 8)] and its exponent to exps[outer * n_inner + inner].
+template <bool FOUR, bool BF16>
+__global__ __launch_bounds__(256) void pack_kernel(const void* __restrict__ src, int64_t n_outer, int64_t n_inner,
+                                                   int64_t s_outer, int64_t s_inner, int64_t s_elem,
+                                                   uint8_t* __restrict__ mant, uint8_t* __restrict__ exps) {
+  int64_t blk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (blk >= n_outer * n_inner) return;
+  int64_t outer = blk / n_inner, inner = blk % n_inner;
+  const int64_t base = inner * s_inner + outer * s_outer;
+  uint32_t bits[16];
+  uint32_t top = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    uint32_t b;
+    if (BF16) b = ((const uint16_t*)src)[base + j * s_elem];
+    else b = bf16_rne(((const uint32_t*)src)[base + j * s_elem]);
+    bits[j] = b;
+    uint32_t e = (b >> 7) & 255u;
+    top = e > top ? e : top;
+  }
+  exps[blk] = (uint8_t)top;
+  if (!FOUR) {
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      uint32_t q = bfp_magnitude(bits[j], top, false);
+      int32_t sq = (bits[j] >> 15) && q ? -(int32_t)q : (int32_t)q;  // no sign on a zero
+      w[j / 4] |= ((uint32_t)sq & 255u) << (8 * (j % 4));
+    }
+    *(uint4*)(mant + blk * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      uint32_t q = bfp_magnitude(bits[j], top, true);
+      int32_t sq = (bits[j] >> 15) && q ? -(int32_t)q : (int32_t)q;
+      w[j / 8] |= ((uint32_t)sq & 15u) << (4 * (j % 8));
+    }
+    *(uint2*)(mant + blk * 8) = make_uint2(w[0], w[1]);
+  }
+}
+
+template <bool FOUR>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ mant, const uint8_t* __restrict__ exps,
+                                                      int64_t n_outer, int64_t n_inner, int64_t s_outer, int64_t s_inner,
+                                                      int64_t s_elem, uint16_t* __restrict__ out) {
+  int64_t blk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (blk >= n_outer * n_inner) return;
+  int64_t outer = blk / n_inner, inner = blk % n_inner;
+  const int64_t base = inner * s_inner + outer * s_outer;
+  uint32_t top = exps[blk];
+  // bfp4's q is worth q * 2^(top - 129) = (16 q) * 2^(top - 133)
+  uint32_t w[4];
+  if (!FOUR) {
+    uint4 v = *(const uint4*)(mant + blk * 16);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else {
+    uint2 v = *(const uint2*)(mant + blk * 8);
+    w[0] = v.x; w[1] = v.y;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    int32_t sq;
+    if (!FOUR) sq = (int8_t)((w[j / 4] >> (8 * (j % 4))) & 255u);
+    else sq = 16 * (((int32_t)((w[j / 8] >> (4 * (j % 8))) << 28)) >> 28);
+    out[base + j * s_elem] = (uint16_t)bfp_value_bf16(sq, top);
+  }
+}
+
+struct BlockGeom {
+  int64_t n_outer, n_inner, s_outer, s_inner, s_elem;
+};
+static int geometry(int64_t K, int64_t N, int64_t ld, int axis, BlockGeom* g) {
+  if (K <= 0 || N <= 0 || ld < N) return fail(FH_EINVAL, "bfp: need K > 0, N > 0 and ld >= N");
+  if (axis == FH_AXIS_N) {
+    if (N % 16) return fail(FH_EINVAL, "bfp along N: N must be a multiple of 16");
+    *g = {N / 16, K, 16, ld, 1};
+  } else if (axis == FH_AXIS_K) {
+    if (K % 16) return fail(FH_EINVAL, "bfp along K: K must be a multiple of 16");
+    *g = {K / 16, N, 16 * ld, 1, ld};
+  } else {
+    return fail(FH_EINVAL, "bfp: axis is FH_AXIS_N or FH_AXIS_K");
+  }
+  return FH_OK;
+}
+
+}  // namespace fh
+
+using namespace fh;
+
+extern "C" const char* fh_last_error(void) { return g_error; }
+
+extern "C" const char* fh_version(void) { return "ferrite_hip 0.1 gfx950"; }
+
+extern "C" int fh_bfp_bytes(int64_t K, int64_t N, int fmt, int axis, size_t* mant_bytes, size_t* exp_bytes) {
+  BlockGeom g;
+  if (int rc = geometry(K, N, N, axis, &g)) return rc;
+  if (fmt != FH_BFP8 && fmt != FH_BFP4) return fail(FH_EINVAL, "bfp: fmt is FH_BFP8 or FH_BFP4");
+  if (mant_bytes) *mant_bytes = (size_t)(K * N) / (fmt == FH_BFP8 ? 1 : 2);
+  if (exp_bytes) *exp_bytes = (size_t)(K * N / 16);
+  return FH_OK;
+}
+
+extern "C" int fh_bfp_pack(const void* src, int src_dtype, int64_t K, int64_t N, int64_t ld, int fmt, int axis,
+                           void* mant, uint8_t* exps, void* stream) {
+  BlockGeom g;
+  if (int rc = geometry(K, N, ld, axis, &g)) return rc;
+  if (!src || !mant || !exps) return fail(FH_EINVAL, "fh_bfp_pack: null pointer");
+  if (src_dtype != FH_F32 && src_dtype != FH_BF16) return fail(FH_EINVAL, "fh_bfp_pack: src is FH_F32 or FH_BF16");
+  if (fmt != FH_BFP8 && fmt != FH_BFP4) return fail(FH_EINVAL, "fh_bfp_pack: fmt is FH_BFP8 or FH_BFP4");
+  int64_t blocks = g.n_outer * g.n_inner;
+  dim3 grid((unsigned)((blocks + 255) / 256)), block(256);
+  hipStream_t s = as_stream(stream);
+  auto m = (uint8_t*)mant;
+  if (fmt == FH_BFP8) {
+    if (src_dtype == FH_F32) hipLaunchKernelGGL((pack_kernel<false, false>), grid, block, 0, s, src, g.n_outer, g.n_inner, g.s_outer, g.s_inner, g.s_elem, m, exps);
+    else hipLaunchKernelGGL((pack_kernel<false, true>), grid, block, 0, s, src, g.n_outer, g.n_inner, g.s_outer, g.s_inner, g.s_elem, m, exps);
+  } else {
+    if (src_dtype == FH_F32) hipLaunchKernelGGL((pack_kernel<true, false>), grid, block, 0, s, src, g.n_outer, g.n_inner, g.s_outer, g.s_inner, g.s_elem, m, exps);
+    else hipLaunchKernelGGL((pack_kernel<true, true>), grid, block, 0, s, src, g.n_outer, g.n_inner, g.s_outer, g.s_inner, g.s_elem, m, exps);
+  }
+  return check_launch("fh_bfp_pack");
+}
+
+extern "C" int fh_bfp_dequant(const void* mant, const uint8_t* exps, int64_t K, int64_t N, int fmt, int axis,
+                              uint16_t* out, int64_t ldo, void* stream) {
+  BlockGeom g;
+  if (int rc = geometry(K, N, ldo, axis, &g)) return rc;
+  if (!mant || !exps || !out) return fail(FH_EINVAL, "fh_bfp_dequant: null pointer");
+  if (fmt != FH_BFP8 && fmt != FH_BFP4) return fail(FH_EINVAL, "fh_bfp_dequant: fmt is FH_BFP8 or FH_BFP4");
+  int64_t blocks = g.n_outer * g.n_inner;
+  dim3 grid((unsigned)((blocks + 255) / 256)), block(256);
+  hipStream_t s = as_stream(stream);
+  if (fmt == FH_BFP8) hipLaunchKernelGGL((dequant_kernel<false>), grid, block, 0, s, (const uint8_t*)mant, exps, g.n_outer, g.n_inner, g.s_outer, g.s_inner, g.s_elem, out);
+  else hipLaunchKernelGGL((dequant_kernel<true>), grid, block, 0, s, (const uint8_t*)mant, exps, g.n_outer, g.n_inner, g.s_outer, g.s_inner, g.s_elem, out);
+  return check_launch("fh_bfp_dequant");
+}
+
+// ---- embedding rows: one workgroup a row --------------------------------------------------------------------------
+template <bool BF16>
+__global__ __launch_bounds__(256) void embed_kernel(const void* __restrict__ table, int64_t vocab, int64_t dim,
+                                                    const int32_t* __restrict__ ids, float* __restrict__ x,
+                                                    float* __restrict__ ssq) {
+  int b = blockIdx.x;
+  int64_t id = ids[b];
+  if (id < 0 || id >= vocab) id = 0;  // (the host checks ids it knows; one computed on the GPU reads row 0 rather than fault)
+  for (int64_t c = threadIdx.x; c < dim; c += blockDim.x) {
+    float v = BF16 ? bf16_to_f(((const uint16_t*)table)[id * dim + c]) : ((const float*)table)[id * dim + c];
+    x[b * dim + c] = v;
+  }
+  __syncthreads();
+  if (ssq) {
+    for (int64_t p = threadIdx.x; p < dim / 16; p += blockDim.x) {
+      float s = 0;
+      for (int j = 0; j < 16; ++j) { float v = x[b * dim + p * 16 + j]; s = fmaf(v, v, s); }
+      ssq[b * (dim / 16) + p] = s;
+    }
+  }
+}
+
+extern "C" int fh_embed_rows(const void* table, int table_dtype, int64_t vocab, int64_t dim, const int32_t* ids,
+                             int batch, float* x, float* ssq_out, void* stream) {
+  if (!table || !ids || !x) return fail(FH_EINVAL, "fh_embed_rows: null pointer");
+  if (vocab <= 0 || dim <= 0 || batch <= 0 || dim % 16) return fail(FH_EINVAL, "fh_embed_rows: bad sizes (dim a multiple of 16)");
+  if (table_dtype != FH_F32 && table_dtype != FH_BF16) return fail(FH_EINVAL, "fh_embed_rows: table is FH_F32 or FH_BF16");
+  hipStream_t s = as_stream(stream);
+  if (table_dtype == FH_BF16) hipLaunchKernelGGL((embed_kernel<true>), dim3(batch), dim3(256), 0, s, table, vocab, dim, ids, x, ssq_out);
+  else hipLaunchKernelGGL((embed_kernel<false>), dim3(batch), dim3(256), 0, s, table, vocab, dim, ids, x, ssq_out);
+  return check_launch("fh_embed_rows");
+}
+
+// ---- argmax of each row: one workgroup a row, the first of equal maxima ------------------------------------------
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int64_t n, int32_t* __restrict__ ids) {
+  const float* row = x + (int64_t)blockIdx.x * n;
+  float best = -INFINITY;
+  int64_t at = n;
+  for (int64_t c = threadIdx.x; c < n; c += blockDim.x) {
+    float v = row[c];
+    if (v > best || (v == best && c < at)) { best = v; at = c; }  // (strictly greater keeps the first of equals)
+  }
+  // wave then workgroup: the larger value, the smaller column on a tie
+  for (int m = 32; m >= 1; m >>= 1) {
+    float ov = __shfl_xor(best, m, 64);
+    int64_t oa = __shfl_xor(at, m, 64);
+    if (ov > best || (ov == best && oa < at)) { best = ov; at = oa; }
+  }
+  __shared__ float bv[16];
+  __shared__ int64_t ba[16];
+  int w = threadIdx.x / 64;
+  if ((threadIdx.x & 63) == 0) { bv[w] = best; ba[w] = at; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < (int)(blockDim.x / 64); ++i)
+      if (bv[i] > best || (bv[i] == best && ba[i] < at)) { best = bv[i]; at = ba[i]; }
+    ids[blockIdx.x] = (int32_t)(at < n ? at : 0);
+  }
+}
+
+extern "C" int fh_argmax_rows(const float* x, int64_t rows, int64_t n, int32_t* ids, void* stream) {
+  if (!x || !ids || rows <= 0 || n <= 0 || n > INT32_MAX) return fail(FH_EINVAL, "fh_argmax_rows: bad arguments");
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(1024), 0, as_stream(stream), x, n, ids);
+  return check_launch("fh_argmax_rows");
+}

@@ -1,0 +1,70 @@
+"""ctypes binding of libferrite_hip.so (include/ferrite_hip.h), in the way ferrite binds libttsim (ferrite/pci.py:18-31):
+explicit argtypes and restype for every entry point, a status code turned into an exception with the library's own
+message. Pointers are plain integers (a torch tensor's data_ptr()), streams the raw hipStream_t (a torch stream's
+cuda_stream). Loading fails loudly when the library is missing: there is no CPU fallback."""
+import ctypes, os, pathlib
+
+HERE = pathlib.Path(__file__).resolve().parent
+PATH = pathlib.Path(os.environ.get("FERRITE_HIP_LIB", HERE / "libferrite_hip.so"))
+
+F32, BF16, BFP8, BFP4, I32 = 0, 1, 2, 3, 4
+AXIS_N, AXIS_K = 0, 1
+EP_STORE, EP_RESIDUAL, EP_SILU_GATE, EP_ROPE_KV = 0, 1, 2, 3
+DTYPES = {"fp32": F32, "bf16": BF16, "bfp8": BFP8, "bfp4": BFP4, "int32": I32}
+ERRORS = {-1: ValueError, -2: NotImplementedError, -3: RuntimeError}
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+L = ctypes.c_int64
+S = ctypes.c_size_t
+
+
+class Epilogue(ctypes.Structure):
+  """fh_epilogue (include/ferrite_hip.h)."""
+  _fields_ = [("kind", I), ("norm_w", P), ("ssq_in", P), ("eps", ctypes.c_float), ("centered", I),
+              ("residual", P), ("ssq_out", P), ("split", I), ("heads", I), ("kv_heads", I), ("head_dim", I),
+              ("cos_tab", P), ("sin_tab", P), ("places", P), ("cache_rows", P), ("cache", P), ("cache_dtype", I),
+              ("cache_len", L)]
+
+
+SIGNATURES = {
+  "fh_last_error": ([], ctypes.c_char_p),
+  "fh_version": ([], ctypes.c_char_p),
+  "fh_bfp_bytes": ([L, L, I, I, ctypes.POINTER(S), ctypes.POINTER(S)], I),
+  "fh_bfp_pack": ([P, I, L, L, L, I, I, P, P, P], I),
+  "fh_bfp_dequant": ([P, P, L, L, I, I, P, L, P], I),
+  "fh_gemv_bfp": ([P, I, L, I, L, L, P, P, I, ctypes.POINTER(Epilogue), P, I, L, P], I),
+  "fh_embed_rows": ([P, I, L, L, P, I, P, P, P], I),
+  "fh_attention_workspace_bytes": ([I, I, I, L], S),
+  "fh_attention_decode": ([P, P, I, L, I, I, I, I, P, P, L, P, P, S, P], I),
+  "fh_argmax_rows": ([P, L, L, P, P], I),
+}
+
+_lib = None
+
+
+def load():
+  """The library, loaded once; raises if it is not built (ferrite_amd.build) or lacks an entry point."""
+  global _lib
+  if _lib is None:
+    if not PATH.exists(): raise RuntimeError(f"{PATH} is not built: run python -m ferrite_amd.build (needs hipcc)")
+    lib = ctypes.CDLL(str(PATH))
+    for name, (args, res) in SIGNATURES.items():
+      fn = getattr(lib, name)
+      fn.argtypes, fn.restype = args, res
+    _lib = lib
+  return _lib
+
+
+def call(name, *args):
+  """Calls an entry point that returns a status; a negative one raises with fh_last_error()'s message."""
+  lib = load()
+  rc = getattr(lib, name)(*args)
+  if rc < 0: raise ERRORS.get(rc, RuntimeError)(lib.fh_last_error().decode())
+  return rc
+
+
+def bfp_bytes(K, N, fmt, axis=AXIS_N):
+  m, e = S(), S()
+  call("fh_bfp_bytes", K, N, fmt, axis, ctypes.byref(m), ctypes.byref(e))
+  return m.value, e.value

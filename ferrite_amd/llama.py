@@ -1,0 +1,194 @@
+"""A Llama decoder on MI355X: models/llama.py's layer structure (layer -> attention / mlp -> mm, models/llama.py:95-146,
+266-269, 459-480) run as the library's fused kernels, a step replayable as one HIP graph (tensor.jit's place,
+ferrite/tensor.py:775-810).
+
+A decode step of `batch` rows (one token of each of `batch` sequences, or a prompt's tokens at consecutive places)
+is, per block:
+  qkv     fh_gemv_bfp  RMSNorm prologue, RoPE on q's and k's heads, k and v put into the cache at each row's place
+  attend  fh_attention_decode over the rows each place reaches
+  o       fh_gemv_bfp  + the residual (x += o), with x's sums of squares for the next norm
+  gate_up fh_gemv_bfp  RMSNorm prologue, silu(gate) * up
+  down    fh_gemv_bfp  + the residual
+then the final norm and the output layer (fp32 logits) and each row's argmax. Activations stay fp32 between
+kernels; weights are block floats (precision's formats); the KV cache is bf16 or fp32.
+"""
+import math
+from types import SimpleNamespace
+import numpy as np
+import torch
+from ferrite_amd import lib, ops
+
+
+def model(**c):
+  """A config: dim, heads, kv, layers, eps, theta, vocab, ffn, places (RoPE rows), head_dim, rope (Llama 3's scaling),
+  tied (output layer = embedding), centered (RMSNorm by 1 + w), as models/llama.py:541-543 keeps them."""
+  d = dict(head_dim=None, rope=None, centered=False, tied=False, places=4096, k=0, experts=0, norm_topk=True)
+  return SimpleNamespace(**(d | c))
+
+
+def head(c): return c.head_dim or c.dim // c.heads
+
+
+def precision(c, mode="bfp8"):
+  """Each matrix's format (models/llama.py:54-76): bfp8 (all), bfp4 (the MLP's gate and up in bfp4), experts (every MLP
+  matrix in bfp4), the rest bfp8. (Fidelity phases are the chip's: products here are exact.)"""
+  four = {"bfp4": ("gate_up",), "tt": ("gate_up",), "experts": ("gate_up", "down")}.get(mode, ())
+  if mode not in ("bfp8", "bfp4", "tt", "experts"): raise ValueError(f"precision: {mode} (the GPU path reads block floats)")
+  p = {(op, l): ("bfp4" if op in four else "bfp8") for l in range(c.layers) for op in ("qkv", "o", "gate_up", "down")}
+  if mode == "tt" and (c.layers, c.dim) == (32, 4096): p["gate_up", 31] = "bfp8"
+  p["head", None] = "bfp8"
+  return p
+
+
+def frequencies(c):
+  """RoPE's inverse frequencies in fp32, Llama 3's scaling if c.rope says llama3 (models/llama.py:333-344)."""
+  hd = head(c)
+  inv = 1 / c.theta ** (np.arange(0, hd, 2, dtype=np.float32) / hd)
+  r = c.rope
+  if r and r.get("rope_type") == "llama3":
+    old, wavelen = r["original_max_position_embeddings"], 2 * math.pi / inv
+    scaled = np.where(wavelen > old / r["low_freq_factor"], inv / r["factor"], inv)
+    smooth = (old / wavelen - r["low_freq_factor"]) / (r["high_freq_factor"] - r["low_freq_factor"])
+    between = (wavelen >= old / r["high_freq_factor"]) & (wavelen <= old / r["low_freq_factor"])
+    inv = np.where(between, (1 - smooth) * scaled / r["factor"] + smooth * scaled, scaled).astype(np.float32)
+  return inv
+
+
+def rotary_tables(c, n):
+  """One head's cos and sin for places 0..n-1, (n, head_dim) fp32 holding bf16 values: fp32 angles rounded to bf16,
+  each half the same (models/llama.py:354-368; the kernel applies them to every q and k head)."""
+  angles = np.arange(n, dtype=np.float32)[:, None] * frequencies(c)[None]
+  def bf16(a):
+    b = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return (((b + 0x7FFF + (b >> 16 & 1)) >> 16 & 0xFFFF).astype(np.uint32) << 16).view(np.float32)
+  return bf16(np.concatenate([np.cos(angles)] * 2, 1)), bf16(np.concatenate([np.sin(angles)] * 2, 1))
+
+
+class Decoder:
+  """The model's weights on the GPU (block floats by precision), its KV cache, and the buffers of a step of `batch`
+  rows. weights(name, shape) gives each weight as a torch fp32 (or bf16) tensor on the GPU, named as models/llama.py's
+  fuse leaves them: layers.{l}.input_layernorm, .post_attention_layernorm, .qkv_proj, .o_proj, .gate_up_proj,
+  .down_proj (x @ w), norm, embed, embed.T (the output layer; the embedding's transpose when tied)."""
+
+  def __init__(self, c, weights, mode="bfp8", kv="bf16", batch=1, context=256, device="cuda", slots=1):
+    self.c, self.mode, self.batch, self.context, self.device = c, mode, batch, context, torch.device(device)
+    self.prec = precision(c, mode)
+    hd = head(c)
+    self.hd, self.qkv_cols = hd, (c.heads + 2 * c.kv) * hd
+    f32 = lambda t: t.to(self.device, torch.float32).contiguous()
+    self.layers = []
+    for l in range(c.layers):
+      pre = f"layers.{l}."
+      L = SimpleNamespace()
+      L.norm1 = f32(weights(pre + "input_layernorm", (1, c.dim))).reshape(-1)
+      L.norm2 = f32(weights(pre + "post_attention_layernorm", (1, c.dim))).reshape(-1)
+      L.qkv = ops.pack(weights(pre + "qkv_proj", (c.dim, self.qkv_cols)), self.prec["qkv", l])
+      L.o = ops.pack(weights(pre + "o_proj", (c.heads * hd, c.dim)), self.prec["o", l])
+      L.gate_up = ops.pack(weights(pre + "gate_up_proj", (c.dim, 2 * c.ffn)), self.prec["gate_up", l])
+      L.down = ops.pack(weights(pre + "down_proj", (c.ffn, c.dim)), self.prec["down", l])
+      self.layers.append(L)
+    self.norm = f32(weights("norm", (1, c.dim))).reshape(-1)
+    embed = weights("embed", (c.vocab, c.dim))
+    self.embed = embed.to(self.device, torch.bfloat16).contiguous()  # bf16 values: a row read per token
+    head_w = embed.to(self.device).t() if c.tied else weights("embed.T", (c.dim, c.vocab))
+    self.head = ops.pack(head_w.contiguous(), self.prec["head", None])
+    cos, sin = rotary_tables(c, c.places)
+    self.cos, self.sin = torch.from_numpy(cos).to(self.device), torch.from_numpy(sin).to(self.device)
+    # the KV cache: a block's keys' heads then values', `slots` sequences' rows side by side (models/llama.py:506-514)
+    self.slots = slots or 1
+    self.part = context  # rows a sequence
+    self.kv_dtype = {"bf16": torch.bfloat16, "fp32": torch.float32}[kv]
+    self.cache = [torch.zeros(2 * c.kv, self.slots * context, hd, dtype=self.kv_dtype, device=self.device) for _ in range(c.layers)]
+    # a step's buffers, fixed so a step replays as a graph
+    B = batch
+    z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.device)
+    self.ids = torch.zeros(B, dtype=torch.int32, device=self.device)
+    self.places = torch.zeros(B, dtype=torch.int32, device=self.device)
+    self.rows = torch.zeros(B, dtype=torch.int32, device=self.device)       # cache row of each row's token
+    self.first = torch.zeros(B, dtype=torch.int32, device=self.device)      # its sequence's first cache row
+    self.x, self.ssq = z(B, c.dim), z(B, c.dim // 16)
+    self.q, self.att = z(B, c.heads * hd), z(B, c.heads * hd)
+    self.h = z(B, c.ffn)
+    self.logits = z(B, c.vocab)
+    self.picks = torch.zeros(B, dtype=torch.int32, device=self.device)
+    self.ws = ops.attention_workspace(B, c.heads, hd, context, self.device)
+    self.graph = None
+
+  def weight_bytes(self):
+    """Bytes of the weights one decode step reads: every matrix, a row of the embedding, the norms."""
+    n = sum(w.nbytes for L in self.layers for w in (L.qkv, L.o, L.gate_up, L.down)) + self.head.nbytes
+    return n + self.c.dim * 2 + (2 * self.c.layers + 1) * self.c.dim * 4
+
+  def set_rows(self, places, slots=None):
+    """Each row's place, and the cache rows: slot s's sequence keeps rows s * context .. (models/llama.py:429-452)."""
+    places = torch.as_tensor(places, dtype=torch.int32)
+    slots = torch.zeros_like(places) if slots is None else torch.as_tensor(slots, dtype=torch.int32)
+    if (places < 0).any() or (places >= min(self.context, self.c.places)).any(): raise ValueError("a place past the cache or RoPE's tables")
+    self.places.copy_(places)
+    self.first.copy_(slots * self.part)
+    self.rows.copy_(slots * self.part + places)
+
+  def _step(self):
+    c, B, hd = self.c, self.batch, self.hd
+    ops.embed_rows(self.embed, self.ids, self.x, self.ssq)
+    for l, L in enumerate(self.layers):
+      ep = ops.epilogue(lib.EP_ROPE_KV, norm_w=L.norm1, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered),
+                        heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
+                        places=self.places, cache_rows=self.rows, cache=self.cache[l],
+                        cache_dtype=lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"], cache_len=self.cache[l].shape[1])
+      ops.gemv(self.x, L.qkv, ep, out=self.q)
+      ops.attention_decode(self.q, self.cache[l], c.heads, c.kv, hd, self.places, self.first, self.context, self.ws, o=self.att)
+      ep = ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq)
+      ops.gemv(self.att, L.o, ep, out=self.x)
+      ep = ops.epilogue(lib.EP_SILU_GATE, norm_w=L.norm2, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered), split=c.ffn)
+      ops.gemv(self.x, L.gate_up, ep, out=self.h)
+      ep = ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq)
+      ops.gemv(self.h, L.down, ep, out=self.x)
+    ep = ops.epilogue(lib.EP_STORE, norm_w=self.norm, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered))
+    ops.gemv(self.x, self.head, ep, out=self.logits)
+    ops.argmax_rows(self.logits, self.picks)
+
+  def step(self, ids=None, places=None, slots=None, replay=True):
+    """One step: the logits (fp32, [batch][vocab]) and picks for tokens ids at places. With replay, the step runs as
+    a HIP graph captured on the first call (every later step launches the same kernels: places are data)."""
+    if ids is not None: self.ids.copy_(torch.as_tensor(ids, dtype=torch.int32))
+    if places is not None: self.set_rows(places, slots)
+    if not replay:
+      self._step()
+    else:
+      if self.graph is None:
+        self._step()  # warm: every kernel loaded before capture
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+          self._step()
+        self.graph = g
+      self.graph.replay()
+    return self.logits, self.picks
+
+  def advance(self):
+    """Each row's next place and its pick as the next token, on the GPU (no host round trip): greedy decoding."""
+    self.ids.copy_(self.picks)
+    self.places.add_(1)
+    self.rows.add_(1)
+
+
+def numpy_weights(w):
+  """weights(name, shape) over a dict of numpy arrays (bf16 values as float32), for Decoder."""
+  def get(name, shape):
+    a = np.asarray(w[name], np.float32).reshape(shape)
+    return torch.from_numpy(np.ascontiguousarray(a))
+  return get
+
+
+def random_weights(c, seed=0, sd=0.02, norm_sd=0.1, embed_sd=1.0, device="cuda"):
+  """weights(name, shape) drawn on the GPU: matrices N(0, sd), norms N(1, norm_sd), the embedding N(0, embed_sd), each
+  rounded to bf16, from a generator seeded by seed and the weight's name (so each is the same whatever asks first)."""
+  def get(name, shape):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed * 1000003 + sum(ord(ch) * 31 ** i for i, ch in enumerate(name)) % (2**31))
+    if "norm" in name: t = torch.randn(*shape, generator=g, device=device) * norm_sd + 1
+    elif name == "embed": t = torch.randn(*shape, generator=g, device=device) * embed_sd
+    else: t = torch.randn(*shape, generator=g, device=device) * sd
+    return t.to(torch.bfloat16)
+  return get

@@ -1,0 +1,115 @@
+"""The hot path's operations on torch tensors resident on the GPU: shape and dtype checks on the host, then one call
+into libferrite_hip.so on torch's current stream. torch is the buffer and stream provider only; every computation is
+a HIP kernel of the library, and a missing library raises (ferrite_amd.lib.load)."""
+import ctypes
+from dataclasses import dataclass
+import torch
+from ferrite_amd import lib
+
+_TORCH = {torch.float32: lib.F32, torch.bfloat16: lib.BF16}
+
+
+def _ptr(t):
+  return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream():
+  return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(*ts):
+  for t in ts:
+    if t is not None and not t.is_cuda: raise ValueError("ferrite_amd: tensors must be on the GPU")
+
+
+@dataclass
+class BfpWeight:
+  """A weight W[K][N] (x @ W) as a block float on the GPU: mant and exps in libferrite_hip's packed layout."""
+  mant: torch.Tensor
+  exps: torch.Tensor
+  K: int
+  N: int
+  fmt: str  # "bfp8" or "bfp4"
+  axis: int = lib.AXIS_N
+
+  @property
+  def nbytes(self): return self.mant.numel() + self.exps.numel()
+
+
+def pack(w, fmt="bfp8", axis=lib.AXIS_N):
+  """w [K][N] (fp32 or bf16, on the GPU) as a block float (fh_bfp_pack)."""
+  _dev(w)
+  if w.dim() != 2: raise ValueError("pack: a matrix")
+  if w.dtype not in _TORCH: raise ValueError("pack: fp32 or bf16")
+  w = w if w.stride(1) == 1 else w.contiguous()
+  K, N = w.shape
+  mb, eb = lib.bfp_bytes(K, N, lib.DTYPES[fmt], axis)
+  mant = torch.empty(mb, dtype=torch.uint8, device=w.device)
+  exps = torch.empty(eb, dtype=torch.uint8, device=w.device)
+  lib.call("fh_bfp_pack", _ptr(w), _TORCH[w.dtype], K, N, w.stride(0), lib.DTYPES[fmt], axis, _ptr(mant), _ptr(exps), _stream())
+  return BfpWeight(mant, exps, K, N, fmt, axis)
+
+
+def dequant(bw, out=None):
+  """The weight's values as bf16 [K][N] (fh_bfp_dequant), bit for bit."""
+  if out is None: out = torch.empty(bw.K, bw.N, dtype=torch.bfloat16, device=bw.mant.device)
+  lib.call("fh_bfp_dequant", _ptr(bw.mant), _ptr(bw.exps), bw.K, bw.N, lib.DTYPES[bw.fmt], bw.axis, _ptr(out), out.stride(0), _stream())
+  return out
+
+
+def epilogue(kind=lib.EP_STORE, **kw):
+  ep = lib.Epilogue()
+  ep.kind = kind
+  for k, v in kw.items():
+    if isinstance(v, torch.Tensor): v = v.data_ptr()
+    setattr(ep, k, v)
+  return ep
+
+
+def gemv(x, bw, ep=None, out=None, out_dtype=torch.float32):
+  """y = x @ W with the epilogue ep (fh_gemv_bfp). x [batch][K] fp32 or bf16; W packed along N."""
+  _dev(x)
+  if bw.axis != lib.AXIS_N: raise NotImplementedError("gemv: weights packed along N")
+  if x.dim() != 2 or x.shape[1] != bw.K or x.stride(1) != 1: raise ValueError(f"gemv: x {tuple(x.shape)} for W {bw.K}x{bw.N}")
+  batch = x.shape[0]
+  if out is None:
+    cols = bw.N
+    if ep is not None and ep.kind == lib.EP_SILU_GATE: cols = ep.split
+    if ep is not None and ep.kind == lib.EP_ROPE_KV: cols = ep.heads * ep.head_dim
+    out = torch.empty(batch, cols, dtype=out_dtype, device=x.device)
+  lib.call("fh_gemv_bfp", _ptr(x), _TORCH[x.dtype], x.stride(0), batch, bw.K, bw.N, _ptr(bw.mant), _ptr(bw.exps),
+           lib.DTYPES[bw.fmt], ctypes.byref(ep) if ep is not None else None, _ptr(out), _TORCH[out.dtype], out.stride(0), _stream())
+  return out
+
+
+def embed_rows(table, ids, x=None, ssq=None):
+  """Rows ids of table into x (fp32), with their sums of squares by runs of 16 (fh_embed_rows)."""
+  _dev(table, ids)
+  vocab, dim = table.shape
+  batch = ids.numel()
+  if x is None: x = torch.empty(batch, dim, dtype=torch.float32, device=table.device)
+  if ssq is None: ssq = torch.empty(batch, dim // 16, dtype=torch.float32, device=table.device)
+  lib.call("fh_embed_rows", _ptr(table), _TORCH[table.dtype], vocab, dim, _ptr(ids), batch, _ptr(x), _ptr(ssq), _stream())
+  return x, ssq
+
+
+def attention_workspace(batch, heads, head_dim, max_context, device="cuda"):
+  n = lib.load().fh_attention_workspace_bytes(batch, heads, head_dim, max_context)
+  return torch.zeros(max(n, 256), dtype=torch.uint8, device=device)
+
+
+def attention_decode(q, cache, heads, kv_heads, head_dim, places, first_row, max_context, workspace, o=None):
+  """softmax(q k^T / sqrt(hd)) v over each row's cache rows (fh_attention_decode). cache [2 kv][len][hd]."""
+  _dev(q, cache, places, first_row)
+  batch = q.shape[0]
+  if o is None: o = torch.empty_like(q)
+  lib.call("fh_attention_decode", _ptr(q), _ptr(cache), _TORCH[cache.dtype], cache.shape[1], batch, heads, kv_heads,
+           head_dim, _ptr(places), _ptr(first_row), max_context, _ptr(o), _ptr(workspace), workspace.numel(), _stream())
+  return o
+
+
+def argmax_rows(x, ids=None):
+  _dev(x)
+  if ids is None: ids = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)
+  lib.call("fh_argmax_rows", _ptr(x), x.shape[0], x.shape[1], _ptr(ids), _stream())
+  return ids

@@ -1,0 +1,137 @@
+/* ferrite_hip.h — the C-ABI of libferrite_hip.so: ferrite's block-float (bfp8/bfp4) weight matmul hot path as
+ * hand-written HIP kernels for gfx950 (MI355X).
+ *
+ * Every entry point takes plain device pointers and sizes, enqueues its kernels on `stream` (a hipStream_t, NULL for the
+ * default stream) and returns at once: 0 on success, a negative FH_E* code otherwise, with the reason in
+ * fh_last_error() (thread-local). Nothing here allocates or frees device memory: the caller owns every buffer, and
+ * scratch comes in through a `workspace` argument sized by the matching *_workspace_bytes call, zero-filled once by
+ * the caller when it is allocated (the kernels leave it zeroed after every call). Calls on one stream run in order;
+ * calls that share a workspace must not overlap.
+ *
+ * The reference (alkinun/ferrite) has no C interface for this path: it builds Tensix kernels in Python
+ * (ferrite/compiler.py) and launches them through ferrite/runtime.py. Each declaration below names the reference
+ * function whose work it replaces.
+ */
+#ifndef FERRITE_HIP_H
+#define FERRITE_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* error codes */
+#define FH_OK 0
+#define FH_EINVAL (-1)   /* bad argument: null pointer, bad size or shape */
+#define FH_EUNSUP (-2)   /* a valid request this build does not support */
+#define FH_EHIP (-3)     /* the HIP runtime reported an error (launch failure, bad stream) */
+
+/* element types */
+#define FH_F32 0
+#define FH_BF16 1
+#define FH_BFP8 2
+#define FH_BFP4 3
+#define FH_I32 4
+
+/* which axis of a weight W[K][N] (x @ W, K rows, N columns) a block of 16 values runs along:
+ * FH_AXIS_N, along a row (16 consecutive columns share an exponent): ferrite's own, gpt2.bfp on W (models/gpt2.py:27,
+ *   models/llama.py:652-653);
+ * FH_AXIS_K, down a column (16 consecutive rows share one): gpt2.bfp(W.T).T. */
+#define FH_AXIS_N 0
+#define FH_AXIS_K 1
+
+/* The last error's message on this thread ("" if none). */
+const char* fh_last_error(void);
+/* The library's version string and the GPU target it was built for. */
+const char* fh_version(void);
+
+/* ---- block-float weights: packing and unpacking ----------------------------------------------------------------
+ * Packed layout of W[K][N] (both axes; for FH_AXIS_K swap the roles of K and N, i.e. the layout of W^T):
+ *   exps: uint8 [N/16][K]            the block's shared exponent (the largest bf16 biased exponent in it)
+ *   mant: bfp8  int8  [N/16][K][16]  the signed magnitude q*sign, -127..127 (two's complement byte)
+ *         bfp4  uint8 [N/16][K][8]   two signed 4-bit magnitudes -7..7 a byte, value 2i in the low nibble
+ * A value is sign * q * 2^(e - 133) (bfp8) or sign * q * 2^(e - 129) (bfp4). */
+
+/* Sizes in bytes of the two arrays for a K x N weight (returns FH_EINVAL for an impossible shape). */
+int fh_bfp_bytes(int64_t K, int64_t N, int fmt, int axis, size_t* mant_bytes, size_t* exp_bytes);
+
+/* Pack src[K][N] (row stride ld elements; FH_F32 or FH_BF16) into a block float: fp32 rounded to bf16 to nearest even,
+ * then each block to its largest exponent, bfp8 keeping 7 bits of magnitude rounded half up and saturated at 127,
+ * bfp4 3 bits rounded to nearest (ties up), saturated at 7, 0 past a shift of 4; a zero keeps no sign.
+ * Replaces Tensor.cast("bfp8"/"bfp4") (ferrite/tensor.py:315-320): the packer's cast (ferrite/compiler.py:52-70) and
+ * bfp4_kernel (ferrite/compiler.py:2038-2072), whose rounding models/gpt2.py:21-32 states. */
+int fh_bfp_pack(const void* src, int src_dtype, int64_t K, int64_t N, int64_t ld, int fmt, int axis, void* mant,
+                uint8_t* exps, void* stream);
+
+/* Unpack to bf16 bits out[K][N] (row stride ldo): each value exactly (every block-float value is a bf16 value).
+ * Replaces tensor._bf16s (ferrite/tensor.py:718-727), the host readback of a block-float tensor. */
+int fh_bfp_dequant(const void* mant, const uint8_t* exps, int64_t K, int64_t N, int fmt, int axis, uint16_t* out,
+                   int64_t ldo, void* stream);
+
+/* ---- decode GEMV: y = x @ W with W a block float, batch 1..16, fused prologue and epilogue ----------------------
+ * x: [batch][K] fp32 or bf16 (row stride ldx). Products are exact and sums are fp32.
+ * Replaces the bfp-B matmul of fused_kernel (ferrite/compiler.py:699-1111, matmul at 958-1022) for a token row
+ * (compiler.py:838-845), with the elementwise ops models/llama.py puts after it fused into the same kernel. */
+
+#define FH_EP_STORE 0      /* y = acc (fp32 or bf16 out, dtype y_dtype) */
+#define FH_EP_RESIDUAL 1   /* y = residual + acc, and the sums of squares of y by 16 columns into ssq_out (if set) */
+#define FH_EP_SILU_GATE 2  /* W's columns are [gate | up], each `split` wide: y[:, j] = silu(gate_j) * up_j, j < split */
+#define FH_EP_ROPE_KV 3    /* W's columns are q, k and v heads: RoPE on q's and k's, q into y, k and v into the cache */
+
+typedef struct fh_epilogue {
+  int kind;                 /* FH_EP_* */
+  /* RMSNorm prologue (models/llama.py:82-85): x is replaced by x * rsqrt(mean(x^2) + eps) * w (n*w + n if centered).
+   * The mean comes from ssq_in: per row, the sums of x^2 over each run of 16 columns ([batch][K/16]), which the
+   * kernel that made x wrote (FH_EP_RESIDUAL's ssq_out, fh_embed_rows). norm_w NULL: no prologue. */
+  const float* norm_w;      /* [K] */
+  const float* ssq_in;      /* [batch][K/16] */
+  float eps;
+  int centered;
+  /* FH_EP_RESIDUAL */
+  const float* residual;    /* [batch][N], row stride ldy; may be y itself */
+  float* ssq_out;           /* [batch][N/16] or NULL */
+  /* FH_EP_SILU_GATE */
+  int split;                /* columns of gate (= of up); y is [batch][split] */
+  /* FH_EP_ROPE_KV (models/llama.py:111-128): heads of q, then k, then v, head_dim each */
+  int heads, kv_heads, head_dim;
+  const float* cos_tab;     /* [places][head_dim]: cos of each place's angles (bf16 values, as rotary makes them) */
+  const float* sin_tab;     /* [places][head_dim] */
+  const int32_t* places;    /* [batch]: each row's place (its rotary row) */
+  const int32_t* cache_rows;/* [batch]: the cache row each row's k and v go to (its slot's first row + place) */
+  void* cache;              /* [2*kv_heads][cache_len][head_dim]: keys' heads then values', fp32 or bf16 */
+  int cache_dtype;
+  int64_t cache_len;
+} fh_epilogue;
+
+/* y (dtype y_dtype, row stride ldy) from x @ W and the epilogue. w_mant/w_exps: a packed [K][N] weight (FH_AXIS_N).
+ * For FH_EP_ROPE_KV, y is q: [batch][heads*head_dim] fp32. */
+int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, int64_t K, int64_t N, const void* w_mant,
+                const uint8_t* w_exps, int fmt, const fh_epilogue* ep, void* y, int y_dtype, int64_t ldy, void* stream);
+
+/* ---- the rest of a decode step ------------------------------------------------------------------------------- */
+
+/* Rows ids[batch] of an embedding table [vocab][dim] (fp32 or bf16) into x[batch][dim] fp32, with the sums of
+ * squares by 16 columns into ssq_out[batch][dim/16] (for the first block's RMSNorm). Replaces the gather of
+ * forward's first line (models/llama.py:472; Tensor.gather, ferrite/tensor.py:116-126). */
+int fh_embed_rows(const void* table, int table_dtype, int64_t vocab, int64_t dim, const int32_t* ids, int batch,
+                  float* x, float* ssq_out, void* stream);
+
+/* Decode attention over a KV cache (models/llama.py:129-142; Tensor.attend, ferrite/tensor.py:487-516): for each
+ * row b and query head h, softmax(q k^T / sqrt(head_dim)) v over the cache rows first_row[b] .. first_row[b] +
+ * places[b] (those its place reaches), k and v the heads of kv head h / (heads / kv_heads) (grouped-query).
+ * q, o: [batch][heads*head_dim] fp32. Flash decoding: the keys are shared out among workgroups in chunks and the
+ * chunks' results combined by exp-weights in the last workgroup to finish (ferrite/compiler.py:1138-1145). */
+size_t fh_attention_workspace_bytes(int batch, int heads, int head_dim, int64_t max_context);
+int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch, int heads,
+                        int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row, int64_t max_context,
+                        float* o, void* workspace, size_t ws_bytes, void* stream);
+
+/* For each row of x[rows][n] (fp32), its largest value's column (the first of equals), into ids[rows]: greedy
+ * decoding's pick (models/llama.py:792, numpy's argmax). */
+int fh_argmax_rows(const float* x, int64_t rows, int64_t n, int32_t* ids, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,95 @@
+"""A whole Llama decode on the GPU (ferrite_amd.llama.Decoder: every kernel through libferrite_hip.so) against the numpy
+restatement of models/llama.py on the same seeded weights: logits close, and greedy tokens identical. The reference's
+tests of the same: test_kv_cache (test/test_sim.py:1451-1469), test_llama_precision (1994-2029), and llama.main's
+check of every step against numpy (models/llama.py:787-796)."""
+import numpy as np
+import pytest
+import torch
+from oracle import bfp as O
+from oracle import llama as OL
+
+pytestmark = pytest.mark.gpu
+
+
+def decoder(c, w, mode, kv, batch=1, context=256):
+  from ferrite_amd import llama as G
+  gc = G.model(**{k: getattr(c, k) for k in ("dim", "heads", "kv", "layers", "eps", "theta", "vocab", "ffn", "places", "rope", "tied")})
+  return G.Decoder(gc, G.numpy_weights(w), mode=mode, kv=kv, batch=batch, context=context)
+
+
+def greedy(c, w, mode, kv, prompt, steps, context):
+  """The numpy model's and the GPU's greedy tokens, each fed its own picks, and the logits of every step."""
+  prec = OL.precision(c, mode, kv)
+  c.precision = prec
+  arrays = OL.arrays(w, prec)
+  # numpy: a bf16 cache holds unrounded values (models/llama.py:127-128); the GPU's rounds them, so the numpy run
+  # that checks a bf16 GPU cache rounds them too, as it does a block-float cache's
+  c.kv_rounded = kv == "bf16"
+  np_kv = OL.kv_cache(c, context)
+  ids = list(prompt)
+  want_logits = []
+  new, places = list(prompt), list(range(len(prompt)))
+  for i in range(steps):
+    logits = OL.forward(new, places, arrays, c, np_kv)[0]
+    want_logits.append(logits)
+    nxt = int(np.argmax(logits))
+    ids.append(nxt)
+    new, places = [nxt], [len(ids) - 1]
+  want = ids[len(prompt):]
+  # the GPU: the prompt as a batch of rows at consecutive places, then a token a step, replayed as a graph
+  dec = decoder(c, w, mode, kv, batch=len(prompt), context=context)
+  logits, picks = dec.step(prompt, list(range(len(prompt))), replay=False)
+  got_logits = [logits[-1].cpu().numpy().astype(np.float64)]
+  got = [int(picks[-1])]
+  one = decoder(c, w, mode, kv, batch=1, context=context)
+  for l in range(c.layers): one.cache[l].copy_(dec.cache[l])
+  one.step([got[-1]], [len(prompt)])
+  for i in range(1, steps):
+    got_logits.append(one.logits[0].cpu().numpy().astype(np.float64))
+    got.append(int(one.picks[0]))
+    one.advance()
+    one.step()
+  return want, got, want_logits, got_logits
+
+
+def smol(layers, vocab, places=256):
+  return OL.smollm(layers=layers, vocab=vocab, places=places)
+
+
+@pytest.mark.parametrize("mode,kv", [("bfp8", "fp32"), ("bfp8", "bf16"), ("bfp4", "bf16")])
+def test_small_decode(cuda, mode, kv):
+  # two SmolLM-shape blocks, a 7-token prompt and 8 greedy steps
+  rng = np.random.default_rng(13)
+  c = smol(2, 512)
+  w = OL.random_weights(c, rng)
+  prompt = [int(i) for i in rng.integers(0, 512, 7)]
+  want, got, wl, gl = greedy(c, w, mode, kv, prompt, 8, 64)
+  for a, b in zip(wl, gl):
+    assert np.abs(a - b).max() <= 1e-3 * np.abs(a).max(), np.abs(a - b).max() / np.abs(a).max()
+  assert got == want, (got, want)
+
+
+def test_replay_is_the_step(cuda):
+  # a replayed step (HIP graph) gives exactly the logits of the same step launched op by op
+  rng = np.random.default_rng(14)
+  c = smol(2, 512)
+  w = OL.random_weights(c, rng)
+  a, b = decoder(c, w, "bfp8", "bf16"), decoder(c, w, "bfp8", "bf16")
+  for i, tok in enumerate([3, 77, 400, 9]):
+    la = a.step([tok], [i], replay=True)[0].cpu().numpy()
+    lb = b.step([tok], [i], replay=False)[0].cpu().numpy()
+    assert np.array_equal(la, lb), i
+
+
+def test_config2_smollm_32_greedy_tokens(cuda):
+  # SmolLM-135M's shape, 30 blocks, vocab 49152, bfp8 weights N(0, 0.02), a bf16 KV cache
+  # prefilled from a 128-token seeded prompt, then 32 greedy steps: the same 32 tokens as numpy
+  rng = np.random.default_rng(2)
+  c = smol(30, 49152, places=256)
+  w = OL.random_weights(c, rng)
+  prompt = [int(i) for i in rng.integers(0, 49152, 128)]
+  want, got, wl, gl = greedy(c, w, "bfp8", "bf16", prompt, 32, 256)
+  worst = max(float(np.abs(a - b).max() / np.abs(a).max()) for a, b in zip(wl, gl))
+  print(f"config 2: logits within {worst:.2e} of their largest; tokens {got[:8]}...")
+  assert got == want, (got, want)
+  assert worst <= 1e-3
