@@ -90,6 +90,50 @@ __device__ inline int reduce_index(int lane, int r) {
 template <int V>
 __device__ inline bool reduce_owner(int lane) { return V >= 64 || (lane & (64 / V - 1)) == 0; }
 
+// DPP and lane-swap moves of gfx950 (a row is 16 lanes)
+template <int CTRL>
+__device__ inline float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int DPP_ROW_MIRROR = 0x140, DPP_ROW_HALF_MIRROR = 0x141, DPP_QUAD_XOR2 = 0x4E, DPP_QUAD_XOR1 = 0xB1;
+// x's upper 32 lanes swapped with y's lower 32; then x holds x[l] (l < 32), y[l - 32] (l >= 32)
+__device__ inline void swap32(float& x, float& y) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  x = __uint_as_float(r[0]); y = __uint_as_float(r[1]);
+}
+// in each 32-lane half, x's upper 16 lanes swapped with y's lower 16
+__device__ inline void swap16(float& x, float& y) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  x = __uint_as_float(r[0]); y = __uint_as_float(r[1]);
+}
+
+// The 16 values a[0..15] of every lane summed over the wave, transposing as it goes: lane l ends with the total of
+// value reduce16_index(l) in a[0] (four lanes, l & 3 = 0..3, hold each). Lane halves swap whole rows for the first two
+// steps (permlane32/16 swaps: no LDS), DPP mirrors pair the lanes of a row for the next two, DPP quad moves finish.
+__device__ inline void wave_reduce16(float (&a)[16]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { swap32(a[i], a[i + 8]); a[i] += a[i + 8]; }  // lanes >= 32: value i + 8
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { swap16(a[i], a[i + 4]); a[i] += a[i + 4]; }  // lanes with bit 4: value i + 4
+  {
+    const bool up = lane & 8;  // partner 15 - l within the row: the other bit-3 half
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float send = up ? a[i] : a[i + 2], keep = up ? a[i + 2] : a[i];
+      a[i] = keep + dpp<DPP_ROW_MIRROR>(send);
+    }
+  }
+  {
+    const bool up = lane & 4;  // partner 7 - l within the half-row: the other bit-2 half
+    const float send = up ? a[0] : a[1], keep = up ? a[1] : a[0];
+    a[0] = keep + dpp<DPP_ROW_HALF_MIRROR>(send);
+  }
+  a[0] += dpp<DPP_QUAD_XOR2>(a[0]);
+  a[0] += dpp<DPP_QUAD_XOR1>(a[0]);
+}
+__device__ inline int reduce16_index(int lane) { return ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1); }
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);

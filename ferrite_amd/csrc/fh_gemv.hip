@@ -1,22 +1,26 @@
 // Decode GEMV by a block-float weight: y = epilogue(prologue(x) @ W), batch 1..8 rows per launch, W packed along N
 // (FH_AXIS_N: 16 columns of a row share an exponent, the layout [N/16][K][16]).
 //
-// A workgroup takes one item (one run of 16 columns, or two paired runs: RoPE's halves of a head, SwiGLU's gate and
-// up) and W waves split its K rows between them. A lane takes one row k of the run at a time: one 16-byte load of the
-// 16 magnitudes, one exponent byte and the row's x values, then for each batch row the x value scaled by the block's
-// 2^(e - 133) (exact) and 16 FMAs, each magnitude converted by one sign-extending byte convert. A wave's 64 lanes read
-// 64 consecutive rows: 1 KiB contiguous (512 B for bfp4). The lanes' 16 x batch x runs partial sums are reduced across
-// the wave by a transposing butterfly, across the waves through LDS in a fixed order, then the epilogue runs on the
-// workgroup's outputs: nothing leaves the kernel but y (and, for RoPE, the cache rows).
+// A workgroup takes one item (one run of 16 columns, or two paired runs: RoPE's halves of a head, SwiGLU's gate and up)
+// and its W waves split the K rows into W slices. A lane takes one row k of a run at a time: one 16-byte load of the
+// 16 magnitudes (8 bytes for bfp4), the exponent byte and the row's x values, then for each batch row x scaled by the
+// block's 2^(e - 133) (exact) and 16 FMAs, each magnitude converted by one sign-extending byte convert. A wave's 64
+// lanes read 64 consecutive rows, 1 KiB contiguous (512 B for bfp4), and keep U such loads in flight. The lanes'
+// partial sums are reduced across the wave by lane swaps and DPP moves (no LDS), across the waves through LDS in a
+// fixed order (results do not depend on timing), and the epilogue runs on the workgroup's outputs. Few registers
+// (about 60 a lane at batch 1) keep ~32 waves on every CU, each with its loads in flight: a decode GEMV is a
+// latency-bound stream, and that is what hides the latency. Nothing crosses workgroups: no atomics, no fences.
 #include <math.h>
+#include <type_traits>
 #include "fh_common.h"
 
 namespace fh {
 
 struct GemvArgs {
-  const void* x; int64_t ldx; int x_bf16;
+  const void* x; int64_t ldx;
   const uint8_t* mant; const uint8_t* exps; int64_t K; int64_t N;
   int pair_half;            // P == 2: the runs of a pair are nb0 and nb0 + pair_half
+  int rows;                 // K in slices of `rows` rows (a multiple of 64), one a wave
   // prologue
   const float* norm_w; const float* ssq_in; int ssq_parts; float eps; int centered;
   // epilogue
@@ -36,141 +40,136 @@ __device__ inline void store_out(void* y, int bf16, int64_t at, float v) {
   else ((float*)y)[at] = v;
 }
 
-// magnitudes of row k of a run, as floats: bfp8's 16 bytes are the signed q; bfp4's 8 bytes give 16 q (the 16 is
+// the 16 magnitudes of a run's row as floats: bfp8's 16 bytes are the signed q; bfp4's 8 bytes give 16 q (the 16 is
 // folded into the scale: q * 2^(e - 129) = 16 q * 2^(e - 133))
-template <bool FOUR>
 __device__ inline void magnitudes(const uint4& m, float (&f)[16]) {
-  if (!FOUR) {
-    const uint32_t w[4] = {m.x, m.y, m.z, m.w};
+  const uint32_t w[4] = {m.x, m.y, m.z, m.w};
 #pragma unroll
-    for (int j = 0; j < 16; ++j) f[j] = (float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 255u);
-  } else {
-    const uint32_t w[2] = {m.x, m.y};
+  for (int j = 0; j < 16; ++j) f[j] = (float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 255u);
+}
+__device__ inline void magnitudes(const uint2& m, float (&f)[16]) {
+  const uint32_t w[2] = {m.x, m.y};
 #pragma unroll
-    for (int d = 0; d < 2; ++d) {
-      uint32_t hi = w[d] & 0xF0F0F0F0u, lo = (w[d] << 4) & 0xF0F0F0F0u;
+  for (int d = 0; d < 2; ++d) {
+    const uint32_t hi = w[d] & 0xF0F0F0F0u, lo = (w[d] << 4) & 0xF0F0F0F0u;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f[8 * d + 2 * i] = (float)(int8_t)((lo >> (8 * i)) & 255u);
-        f[8 * d + 2 * i + 1] = (float)(int8_t)((hi >> (8 * i)) & 255u);
-      }
+    for (int i = 0; i < 4; ++i) {
+      f[8 * d + 2 * i] = (float)(int8_t)((lo >> (8 * i)) & 255u);
+      f[8 * d + 2 * i + 1] = (float)(int8_t)((hi >> (8 * i)) & 255u);
     }
   }
 }
 
-template <bool FOUR, int B, int P, bool NORM, bool XBF>
-__global__ __launch_bounds__(512) void gemv_kernel(GemvArgs a) {
-  constexpr int V = B * P * 16;                 // a lane's partial sums: [b][p][j]
-  constexpr int U = (B * P <= 2) ? 8 : 4;       // rows a lane has in flight
-  constexpr int RB = FOUR ? 8 : 16;             // bytes of a run's row
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
-  const int item = blockIdx.x;
+// rows a lane has in flight at once, by format and batch rows (about 4 KiB of weight a wave for one batch row)
+__host__ __device__ constexpr int gemv_group(bool four, int b) { return (b <= 2 ? 4 : b <= 4 ? 2 : 1) * (four ? 2 : 1); }
+
+template <bool FOUR, int B, int P, bool NORM>
+__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
+  constexpr int V = B * P * 16;       // a lane's partial sums: [b][p][j]
+  constexpr int G = B * P;
+  constexpr int U = gemv_group(FOUR, B);
+  constexpr int RB = FOUR ? 8 : 16;   // bytes of a run's row
+  using Row = typename std::conditional<FOUR, uint2, uint4>::type;
+  const int lane = threadIdx.x & 63;
+  const int slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6, item = blockIdx.x;
   int64_t nb[P];
   if (P == 1) nb[0] = item;
   else { nb[0] = (int64_t)(item / a.pair_half) * (2 * a.pair_half) + item % a.pair_half; nb[P - 1] = nb[0] + a.pair_half; }
-  const int64_t K = a.K;
-  const int64_t nchunks = (K + 63) / 64;
-  const int64_t c0 = wave * nchunks / W, c1 = (wave + 1) * nchunks / W;
+  const int K = (int)a.K;             // (the host keeps K below 2^27)
+  const int r0 = slice * a.rows, r1 = min(K, r0 + a.rows);
 
   const uint8_t* mb[P];
   const uint8_t* eb[P];
 #pragma unroll
-  for (int p = 0; p < P; ++p) { mb[p] = a.mant + nb[p] * K * RB; eb[p] = a.exps + nb[p] * K; }
+  for (int p = 0; p < P; ++p) { mb[p] = a.mant + nb[p] * a.K * RB; eb[p] = a.exps + nb[p] * a.K; }
   const float* xf = (const float*)a.x;
-  const uint16_t* xh = (const uint16_t*)a.x;
+  const int ldx = (int)a.ldx;
 
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.f;
 
-  uint4 mv[U][P];
-  int ev[U][P];
-  float xv[U][B];
-  // one row k of every run and of x into slot u
-  auto load = [&](int u, int64_t k) {
+  // U rows of each run, 64 apart, a lane; rows past r1 are read at r1 - 1 (they exist) and count as 0
+  for (int k0 = r0; k0 < r1; k0 += 64 * U) {
+    Row m[U][P];
+    int e[U][P];
+    float xv[U][B], g[U];
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      if (!FOUR) mv[u][p] = *(const uint4*)(mb[p] + k * 16);
-      else { uint2 t = *(const uint2*)(mb[p] + k * 8); mv[u][p] = make_uint4(t.x, t.y, 0, 0); }
-      ev[u][p] = eb[p][k];
+    for (int u = 0; u < U; ++u) {
+      const int k = min(k0 + 64 * u + lane, r1 - 1);
+#pragma unroll
+      for (int p = 0; p < P; ++p) { m[u][p] = *(const Row*)(mb[p] + (uint32_t)k * RB); e[u][p] = eb[p][k]; }
+      if (NORM) g[u] = a.norm_w[k];
+#pragma unroll
+      for (int b = 0; b < B; ++b) xv[u][b] = xf[b * ldx + k];
     }
-    float g = 1.f;
-    if (NORM) { g = a.norm_w[k]; if (a.centered) g += 1.f; }
+    __builtin_amdgcn_sched_barrier(0);  // every load above in flight before any arithmetic
 #pragma unroll
-    for (int b = 0; b < B; ++b) xv[u][b] = (XBF ? bf16_to_f(xh[b * a.ldx + k]) : xf[b * a.ldx + k]) * g;
-  };
-  auto clear = [&](int u) {
+    for (int u = 0; u < U; ++u) {
+      const bool ok = k0 + 64 * u + lane < r1;
+      float gw = 1.f;
+      if (NORM) gw = a.centered ? g[u] + 1.f : g[u];
 #pragma unroll
-    for (int p = 0; p < P; ++p) { mv[u][p] = make_uint4(0, 0, 0, 0); ev[u][p] = 133; }
+      for (int p = 0; p < P; ++p) {
+        float f[16];
+        magnitudes(m[u][p], f);
+        float xs[B];
 #pragma unroll
-    for (int b = 0; b < B; ++b) xv[u][b] = 0.f;
-  };
-  auto compute = [&](int u) {
+        for (int b = 0; b < B; ++b) xs[b] = ok ? ldexpf(xv[u][b] * gw, e[u][p] - 133) : 0.f;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      float f[16];
-      magnitudes<FOUR>(mv[u][p], f);
-      float xs[B];
+        for (int j = 0; j < 16; ++j)
 #pragma unroll
-      for (int b = 0; b < B; ++b) xs[b] = ldexpf(xv[u][b], ev[u][p] - 133);
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-#pragma unroll
-        for (int b = 0; b < B; ++b) acc[(b * P + p) * 16 + j] = fmaf(xs[b], f[j], acc[(b * P + p) * 16 + j]);
-    }
-  };
-
-  for (int64_t c = c0; c < c1; c += U) {
-    if (c + U <= c1 && (c + U) * 64 <= K) {  // U whole chunks: every load at once, unguarded
-#pragma unroll
-      for (int u = 0; u < U; ++u) load(u, (c + u) * 64 + lane);
-#pragma unroll
-      for (int u = 0; u < U; ++u) compute(u);
-    } else {  // the wave's last chunks: the same, each chunk only if it is the wave's, each row only below K
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t k = (c + u) * 64 + lane;
-        if (c + u < c1 && k < K) load(u, k);
-        else clear(u);
+          for (int b = 0; b < B; ++b) acc[(b * P + p) * 16 + j] = fmaf(xs[b], f[j], acc[(b * P + p) * 16 + j]);
       }
-#pragma unroll
-      for (int u = 0; u < U; ++u) compute(u);
     }
   }
 
-  // across the wave, then the waves in order
-  wave_reduce_transpose<V>(acc);
-  __shared__ float red[8][V];
-  __shared__ float fin[V];
-  __shared__ float rscale[B];
-  if (reduce_owner<V>(lane)) {
+  // each run of 16 across the wave: lane holds the sum of value reduce16_index(lane) of each group in sums[g]
+  float sums[G];
 #pragma unroll
-    for (int r = 0; r < (V >= 64 ? V / 64 : 1); ++r) red[wave][reduce_index<V>(lane, r)] = acc[r];
+  for (int gi = 0; gi < G; ++gi) {
+    float r16[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) r16[j] = acc[gi * 16 + j];
+    wave_reduce16(r16);
+    sums[gi] = r16[0];
   }
-  if (a.norm_w && wave == 0) {  // each row's 1 / rms from the sums of squares its maker left by runs of 16
-    for (int b = 0; b < B; ++b) {
+  const int j16 = reduce16_index(lane);
+  __shared__ float red[16][V];
+  __shared__ float fin[V];
+  if ((lane & 3) == 0) {
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) red[slice][gi * 16 + j16] = sums[gi];
+  }
+  __syncthreads();
+  if (slice != 0) return;  // wave 0 adds the slices in order and runs the epilogue
+  for (int i = lane; i < V; i += 64) {
+    float t = red[0][i];
+    for (int w = 1; w < W; ++w) t += red[w][i];
+    fin[i] = t;
+  }
+  // each batch row's 1 / rms, from the sums of squares its maker left by runs of 16
+  float rs[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    rs[b] = 1.f;
+    if (NORM) {
       float s = 0.f;
       for (int i = lane; i < a.ssq_parts; i += 64) s += a.ssq_in[(int64_t)b * a.ssq_parts + i];
       s = wave_sum(s);
-      if (lane == 0) rscale[b] = 1.0f / sqrtf(s / (float)K + a.eps);
+      rs[b] = 1.0f / sqrtf(s / (float)K + a.eps);
     }
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < V; i += blockDim.x) {
-    float s = red[0][i];
-    for (int w = 1; w < W; ++w) s += red[w][i];
-    if (a.norm_w) s *= rscale[i / (P * 16)];
-    fin[i] = s;
-  }
-  __syncthreads();
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 
-  // the epilogue, a thread an output (or a pair of them)
+  // the epilogue, a lane an output (or a pair of them)
   const int kind = a.kind;
   if (kind == FH_EP_STORE || kind == FH_EP_RESIDUAL) {
-    for (int i = threadIdx.x; i < V; i += blockDim.x) {  // V is a multiple of 16 and of the 64-thread waves' groups
+    for (int i = lane; i < V; i += 64) {  // (V is a multiple of 16: a run's 16 values are 16 neighbouring lanes)
       const int b = i / (P * 16), p = (i / 16) % P, j = i % 16;
       const int64_t col = nb[p] * 16 + j, at = b * a.ldy + col;
-      float v = fin[i];
+      float v = fin[i] * (NORM ? rs[b] : 1.f);
       if (kind == FH_EP_RESIDUAL) v += a.residual[at];
       store_out(a.y, a.y_bf16, at, v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
@@ -180,24 +179,26 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvArgs a) {
       }
     }
   } else if (P == 2 && kind == FH_EP_SILU_GATE) {
-    for (int i = threadIdx.x; i < B * 16; i += blockDim.x) {
+    for (int i = lane; i < B * 16; i += 64) {
       const int b = i / 16, j = i % 16;
-      const float g = fin[(b * P) * 16 + j], u = fin[(b * P + 1) * 16 + j];
-      store_out(a.y, a.y_bf16, b * a.ldy + nb[0] * 16 + j, silu(g) * u);
+      const float r = NORM ? rs[b] : 1.f;
+      const float gv = fin[(b * P) * 16 + j] * r, uv = fin[(b * P + 1) * 16 + j] * r;
+      store_out(a.y, a.y_bf16, b * a.ldy + nb[0] * 16 + j, silu(gv) * uv);
     }
   } else if (P == 2 && kind == FH_EP_ROPE_KV) {
     const int hd = a.head_dim;
-    for (int i = threadIdx.x; i < B * 16; i += blockDim.x) {
+    for (int i = lane; i < B * 16; i += 64) {
       const int b = i / 16, j = i % 16;
       const int64_t c0 = nb[0] * 16 + j;            // in the first half of its head
       const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
-      float x0 = fin[(b * P) * 16 + j], x1 = fin[(b * P + 1) * 16 + j];
+      const float r = NORM ? rs[b] : 1.f;
+      float x0 = fin[(b * P) * 16 + j] * r, x1 = fin[(b * P + 1) * 16 + j] * r;
       const int place = a.places[b];
       if (h < a.heads + a.kv_heads) {  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
         const float* cs = a.cos_tab + (int64_t)place * hd;
         const float* sn = a.sin_tab + (int64_t)place * hd;
-        const float r0 = x0 * cs[d] - x1 * sn[d], r1 = x1 * cs[d1] + x0 * sn[d1];
-        x0 = r0; x1 = r1;
+        const float t0 = x0 * cs[d] - x1 * sn[d], t1 = x1 * cs[d1] + x0 * sn[d1];
+        x0 = t0; x1 = t1;
       }
       if (h < a.heads) {
         float* q = (float*)a.y + b * a.ldy + (int64_t)h * hd;
@@ -215,9 +216,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvArgs a) {
 template <bool FOUR, int B, int P>
 static void launch(const GemvArgs& a, int items, int W, hipStream_t s) {
   const dim3 g(items), t(64 * W);
-  if (a.norm_w) hipLaunchKernelGGL((gemv_kernel<FOUR, B, P, true, false>), g, t, 0, s, a);
-  else if (a.x_bf16) hipLaunchKernelGGL((gemv_kernel<FOUR, B, P, false, true>), g, t, 0, s, a);
-  else hipLaunchKernelGGL((gemv_kernel<FOUR, B, P, false, false>), g, t, 0, s, a);
+  if (a.norm_w) hipLaunchKernelGGL((gemv_kernel<FOUR, B, P, true>), g, t, 0, s, a);
+  else hipLaunchKernelGGL((gemv_kernel<FOUR, B, P, false>), g, t, 0, s, a);
 }
 
 template <bool FOUR, int P>
@@ -243,14 +243,25 @@ static int dispatch_batch(const GemvArgs& a, int batch, int items, int W, hipStr
   return FH_OK;
 }
 
-// Waves per workgroup: enough workgroups x waves to keep every CU's memory pipe busy (about 10 waves a CU on 256
-// CUs), at most 8 and no more than the K rows' 64-row chunks.
-static int waves_for(int64_t items, int64_t K) {
-  int64_t chunks = (K + 63) / 64;
-  int64_t w = (2560 + items - 1) / items;
-  if (w > 8) w = 8;
-  if (w > chunks) w = chunks;
-  return w < 1 ? 1 : (int)w;
+// The K slices: W waves a workgroup, the least power of 2 giving about 16384 waves in all (64 a CU on 256 CUs, in
+// turns), at most 16 and at most one a group of U loads of 64 rows a lane.
+struct Plan { int W, rows, P, most, items; };
+static Plan plan(int64_t K, int64_t N, int fmt, int kind, int batch) {
+  Plan p;
+  p.P = (kind == FH_EP_SILU_GATE || kind == FH_EP_ROPE_KV) ? 2 : 1;
+  p.most = p.P == 1 ? 8 : 4;
+  p.items = (int)(N / 16 / p.P);
+  const int b = batch < p.most ? batch : p.most;
+  const int unit = 64 * gemv_group(fmt == FH_BFP4, b);
+  const int64_t units = (K + unit - 1) / unit;
+  int64_t W = 1;
+  while (W < 16 && W * p.items < 16384) W *= 2;
+  while (W > 1 && W > units) W /= 2;
+  int64_t rows = (K + W - 1) / W;
+  rows = (rows + 63) / 64 * 64;
+  p.W = (int)((K + rows - 1) / rows);
+  p.rows = (int)rows;
+  return p;
 }
 
 }  // namespace fh
@@ -262,21 +273,20 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
                            void* stream) {
   if (!x || !w_mant || !w_exps || !y) return fail(FH_EINVAL, "fh_gemv_bfp: null pointer");
   if (batch < 1 || K < 1 || N < 16 || N % 16) return fail(FH_EINVAL, "fh_gemv_bfp: need batch >= 1, K >= 1, N a multiple of 16");
-  if (x_dtype != FH_F32 && x_dtype != FH_BF16) return fail(FH_EINVAL, "fh_gemv_bfp: x is FH_F32 or FH_BF16");
+  if (x_dtype != FH_F32) return fail(FH_EUNSUP, "fh_gemv_bfp: x is FH_F32 (activations stay fp32 between kernels)");
   if (y_dtype != FH_F32 && y_dtype != FH_BF16) return fail(FH_EINVAL, "fh_gemv_bfp: y is FH_F32 or FH_BF16");
   if (fmt != FH_BFP8 && fmt != FH_BFP4) return fail(FH_EINVAL, "fh_gemv_bfp: fmt is FH_BFP8 or FH_BFP4");
   if (ldx < K) return fail(FH_EINVAL, "fh_gemv_bfp: ldx < K");
+  if (K >= (1LL << 27) || (int64_t)batch * ldx >= (1LL << 31)) return fail(FH_EUNSUP, "fh_gemv_bfp: K or x too large for 32-bit row offsets");
   GemvArgs a = {};
-  a.x = x; a.ldx = ldx; a.x_bf16 = x_dtype == FH_BF16;
+  a.x = x; a.ldx = ldx;
   a.mant = (const uint8_t*)w_mant; a.exps = w_exps; a.K = K; a.N = N;
   a.y = y; a.y_bf16 = y_dtype == FH_BF16; a.ldy = ldy;
   a.kind = ep ? ep->kind : FH_EP_STORE;
-  int P = 1;
   int64_t out_cols = N;
   if (ep) {
     if (ep->norm_w) {
       if (!ep->ssq_in || K % 16) return fail(FH_EINVAL, "fh_gemv_bfp: RMSNorm prologue needs ssq_in and K a multiple of 16");
-      if (x_dtype != FH_F32) return fail(FH_EUNSUP, "fh_gemv_bfp: the RMSNorm prologue takes fp32 x");
       a.norm_w = ep->norm_w; a.ssq_in = ep->ssq_in; a.ssq_parts = (int)(K / 16); a.eps = ep->eps; a.centered = ep->centered;
     }
     switch (ep->kind) {
@@ -288,7 +298,7 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
         break;
       case FH_EP_SILU_GATE:
         if (ep->split * 2 != N || ep->split % 16) return fail(FH_EINVAL, "fh_gemv_bfp: FH_EP_SILU_GATE needs N = 2 * split, split a multiple of 16");
-        P = 2; a.pair_half = ep->split / 16; a.split = ep->split; out_cols = ep->split;
+        a.pair_half = ep->split / 16; a.split = ep->split; out_cols = ep->split;
         break;
       case FH_EP_ROPE_KV: {
         const int hd = ep->head_dim;
@@ -298,7 +308,7 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
           return fail(FH_EINVAL, "fh_gemv_bfp: FH_EP_ROPE_KV needs tables, places, cache rows and a cache");
         if (ep->cache_dtype != FH_F32 && ep->cache_dtype != FH_BF16) return fail(FH_EUNSUP, "fh_gemv_bfp: cache is FH_F32 or FH_BF16");
         if (y_dtype != FH_F32) return fail(FH_EUNSUP, "fh_gemv_bfp: FH_EP_ROPE_KV writes q in fp32");
-        P = 2; a.pair_half = hd / 32; out_cols = (int64_t)ep->heads * hd;
+        a.pair_half = hd / 32; out_cols = (int64_t)ep->heads * hd;
         a.heads = ep->heads; a.kv_heads = ep->kv_heads; a.head_dim = hd;
         a.cos_tab = ep->cos_tab; a.sin_tab = ep->sin_tab; a.places = ep->places; a.cache_rows = ep->cache_rows;
         a.cache = ep->cache; a.cache_bf16 = ep->cache_dtype == FH_BF16; a.cache_len = ep->cache_len;
@@ -308,23 +318,21 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
     }
   }
   if (ldy < out_cols) return fail(FH_EINVAL, "fh_gemv_bfp: ldy smaller than the output's columns");
-  const int64_t items = N / 16 / P;
-  if (items > INT32_MAX) return fail(FH_EINVAL, "fh_gemv_bfp: N too large");
-  const int W = waves_for(items, K);
+  const Plan p = plan(K, N, fmt, a.kind, batch);
+  a.rows = p.rows;
   hipStream_t s = as_stream(stream);
-  const int most = P == 1 ? 8 : 4;  // rows a launch takes; more go in several launches, each reading W again
   const bool four = fmt == FH_BFP4;
-  for (int b0 = 0; b0 < batch; b0 += most) {
-    const int n = batch - b0 < most ? batch - b0 : most;
+  for (int b0 = 0; b0 < batch; b0 += p.most) {  // more rows than a launch takes: several launches, each reading W again
+    const int n = batch - b0 < p.most ? batch - b0 : p.most;
     GemvArgs c = a;
-    c.x = (const char*)x + (size_t)b0 * ldx * (a.x_bf16 ? 2 : 4);
+    c.x = (const char*)x + (size_t)b0 * ldx * 4;
     c.y = (char*)y + (size_t)b0 * ldy * (a.y_bf16 ? 2 : 4);
     if (c.ssq_in) c.ssq_in += (int64_t)b0 * c.ssq_parts;
     if (c.residual) c.residual += (int64_t)b0 * ldy;
     if (c.ssq_out) c.ssq_out += (int64_t)b0 * (N / 16);
     if (c.places) { c.places += b0; c.cache_rows += b0; }
-    int rc = P == 1 ? (four ? dispatch_batch<true, 1>(c, n, (int)items, W, s) : dispatch_batch<false, 1>(c, n, (int)items, W, s))
-                    : (four ? dispatch_batch<true, 2>(c, n, (int)items, W, s) : dispatch_batch<false, 2>(c, n, (int)items, W, s));
+    int rc = p.P == 1 ? (four ? dispatch_batch<true, 1>(c, n, p.items, p.W, s) : dispatch_batch<false, 1>(c, n, p.items, p.W, s))
+                      : (four ? dispatch_batch<true, 2>(c, n, p.items, p.W, s) : dispatch_batch<false, 2>(c, n, p.items, p.W, s));
     if (rc) return rc;
     if ((rc = check_launch("fh_gemv_bfp"))) return rc;
   }

@@ -76,21 +76,22 @@ class Decoder:
     hd = head(c)
     self.hd, self.qkv_cols = hd, (c.heads + 2 * c.kv) * hd
     f32 = lambda t: t.to(self.device, torch.float32).contiguous()
+    gpu = lambda t: t.to(self.device)
     self.layers = []
     for l in range(c.layers):
       pre = f"layers.{l}."
       L = SimpleNamespace()
       L.norm1 = f32(weights(pre + "input_layernorm", (1, c.dim))).reshape(-1)
       L.norm2 = f32(weights(pre + "post_attention_layernorm", (1, c.dim))).reshape(-1)
-      L.qkv = ops.pack(weights(pre + "qkv_proj", (c.dim, self.qkv_cols)), self.prec["qkv", l])
-      L.o = ops.pack(weights(pre + "o_proj", (c.heads * hd, c.dim)), self.prec["o", l])
-      L.gate_up = ops.pack(weights(pre + "gate_up_proj", (c.dim, 2 * c.ffn)), self.prec["gate_up", l])
-      L.down = ops.pack(weights(pre + "down_proj", (c.ffn, c.dim)), self.prec["down", l])
+      L.qkv = ops.pack(gpu(weights(pre + "qkv_proj", (c.dim, self.qkv_cols))), self.prec["qkv", l])
+      L.o = ops.pack(gpu(weights(pre + "o_proj", (c.heads * hd, c.dim))), self.prec["o", l])
+      L.gate_up = ops.pack(gpu(weights(pre + "gate_up_proj", (c.dim, 2 * c.ffn))), self.prec["gate_up", l])
+      L.down = ops.pack(gpu(weights(pre + "down_proj", (c.ffn, c.dim))), self.prec["down", l])
       self.layers.append(L)
     self.norm = f32(weights("norm", (1, c.dim))).reshape(-1)
     embed = weights("embed", (c.vocab, c.dim))
     self.embed = embed.to(self.device, torch.bfloat16).contiguous()  # bf16 values: a row read per token
-    head_w = embed.to(self.device).t() if c.tied else weights("embed.T", (c.dim, c.vocab))
+    head_w = embed.to(self.device).t() if c.tied else gpu(weights("embed.T", (c.dim, c.vocab)))
     self.head = ops.pack(head_w.contiguous(), self.prec["head", None])
     cos, sin = rotary_tables(c, c.places)
     self.cos, self.sin = torch.from_numpy(cos).to(self.device), torch.from_numpy(sin).to(self.device)

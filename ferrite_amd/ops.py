@@ -58,16 +58,21 @@ def dequant(bw, out=None):
 
 
 def epilogue(kind=lib.EP_STORE, **kw):
+  """An fh_epilogue; tensors given are kept alive with it (the kernel reads them when it runs, after this returns)."""
   ep = lib.Epilogue()
   ep.kind = kind
+  ep.keep = []
   for k, v in kw.items():
-    if isinstance(v, torch.Tensor): v = v.data_ptr()
+    if isinstance(v, torch.Tensor):
+      _dev(v)
+      ep.keep.append(v)
+      v = v.data_ptr()
     setattr(ep, k, v)
   return ep
 
 
 def gemv(x, bw, ep=None, out=None, out_dtype=torch.float32):
-  """y = x @ W with the epilogue ep (fh_gemv_bfp). x [batch][K] fp32 or bf16; W packed along N."""
+  """y = x @ W with the epilogue ep (fh_gemv_bfp). x [batch][K] fp32; W packed along N."""
   _dev(x)
   if bw.axis != lib.AXIS_N: raise NotImplementedError("gemv: weights packed along N")
   if x.dim() != 2 or x.shape[1] != bw.K or x.stride(1) != 1: raise ValueError(f"gemv: x {tuple(x.shape)} for W {bw.K}x{bw.N}")
@@ -78,7 +83,8 @@ def gemv(x, bw, ep=None, out=None, out_dtype=torch.float32):
     if ep is not None and ep.kind == lib.EP_ROPE_KV: cols = ep.heads * ep.head_dim
     out = torch.empty(batch, cols, dtype=out_dtype, device=x.device)
   lib.call("fh_gemv_bfp", _ptr(x), _TORCH[x.dtype], x.stride(0), batch, bw.K, bw.N, _ptr(bw.mant), _ptr(bw.exps),
-           lib.DTYPES[bw.fmt], ctypes.byref(ep) if ep is not None else None, _ptr(out), _TORCH[out.dtype], out.stride(0), _stream())
+           lib.DTYPES[bw.fmt], ctypes.byref(ep) if ep is not None else None, _ptr(out), _TORCH[out.dtype], out.stride(0),
+           _stream())
   return out
 
 

@@ -70,7 +70,7 @@ int fh_bfp_dequant(const void* mant, const uint8_t* exps, int64_t K, int64_t N, 
                    int64_t ldo, void* stream);
 
 /* ---- decode GEMV: y = x @ W with W a block float, batch 1..16, fused prologue and epilogue ----------------------
- * x: [batch][K] fp32 or bf16 (row stride ldx). Products are exact and sums are fp32.
+ * x: [batch][K] fp32 (row stride ldx). Products are exact and sums are fp32.
  * Replaces the bfp-B matmul of fused_kernel (ferrite/compiler.py:699-1111, matmul at 958-1022) for a token row
  * (compiler.py:838-845), with the elementwise ops models/llama.py puts after it fused into the same kernel. */
 
@@ -104,8 +104,9 @@ typedef struct fh_epilogue {
   int64_t cache_len;
 } fh_epilogue;
 
-/* y (dtype y_dtype, row stride ldy) from x @ W and the epilogue. w_mant/w_exps: a packed [K][N] weight (FH_AXIS_N).
- * For FH_EP_ROPE_KV, y is q: [batch][heads*head_dim] fp32. */
+/* y (dtype y_dtype, row stride ldy) from x @ W and the epilogue. x: fp32. w_mant/w_exps: a packed [K][N] weight
+ * (FH_AXIS_N). For FH_EP_ROPE_KV, y is q: [batch][heads*head_dim] fp32. K is split among the waves of a workgroup,
+ * whose sums meet in a fixed order (results do not depend on timing); no scratch memory is needed. */
 int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, int64_t K, int64_t N, const void* w_mant,
                 const uint8_t* w_exps, int fmt, const fh_epilogue* ep, void* y, int y_dtype, int64_t ldy, void* stream);
 

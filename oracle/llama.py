@@ -144,8 +144,8 @@ def attention(h, p, c, tables, mask, cache, rows):
   heads = split(qkv, nh)
   kv = heads[c.heads:]
   fmt = (c.precision or {}).get(("kv", None), ("bf16", None))[0]
-  if fmt != "bf16": kv = bfp(kv, fmt)  # (llama.py:127-128: numpy rounds a block-float cache as the chip does)
-  elif getattr(c, "kv_rounded", False): kv = bf16(kv)  # a bf16 cache as a GPU (or the chip) keeps it; llama.py's doesn't
+  if fmt in ("bfp8", "bfp4"): kv = bfp(kv, fmt)  # (llama.py:127-128: numpy rounds a block-float cache as the chip does)
+  elif fmt == "bf16" and getattr(c, "kv_rounded", False): kv = bf16(kv)  # a bf16 cache as a GPU (or the chip) keeps it; llama.py's doesn't
   cache[:, list(rows)] = kv
   q, k, v = heads[:c.heads], cache[:c.kv], cache[c.kv:]
   m = mask.shape[-1]
