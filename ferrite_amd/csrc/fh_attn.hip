@@ -1,17 +1,18 @@
-// Decode attention over a KV cache, flash-decoding style. A workgroup (four waves) takes a chunk of 256 cache rows of one
-// key/value head of one batch row and all the query heads that share it (grouped-query: heads / kv_heads of them):
-// each lane scores one row against every query head, the wave takes the chunk's largest score and sum of exps, then
-// each lane accumulates p * v over the chunk for its dimensions. A chunk's (max, sum, p v) goes to the workspace; the
-// last chunk to finish (an atomic count per batch row and key head, reset by that workgroup) weights each chunk by
-// exp(its max - the largest) and writes o. A row reads only the cache rows its place reaches.
+// Decode attention over a KV cache, flash-decoding style, in two kernels. The first: a workgroup (two waves) takes a
+// chunk of 128 cache rows of one batch row for one query head (grouped-query: its key head is h / (heads / kv_heads);
+// the query heads that share a key head read the same rows, which the Infinity Cache serves after the first); each
+// lane scores one row (its keys' loads all in flight), the wave takes its largest score and sum of exps, then each
+// lane accumulates p * v for its dimensions (the wave's 64 rows of values loaded one row per instruction, all in
+// flight); the waves meet in LDS and the chunk's (max, sum, p v) goes to the workspace, or, when the row's keys fit one
+// chunk, o itself. The second kernel combines the chunks of each (row, head) by exp(max - the largest). A kernel
+// boundary, not a fence, orders the two. A row reads only the cache rows its place reaches.
 #include <math.h>
 #include "fh_common.h"
 
 namespace fh {
 
-constexpr int ATT_WAVES = 4;                 // waves a workgroup, 64 cache rows each
+constexpr int ATT_WAVES = 2;                 // waves a workgroup, 64 cache rows each
 constexpr int ATT_CHUNK = 64 * ATT_WAVES;    // cache rows a workgroup
-constexpr int ATT_MAX_REP = 8;
 
 struct AttArgs {
   const float* q; const void* cache; int64_t cache_len;
@@ -19,133 +20,131 @@ struct AttArgs {
   const int32_t* places; const int32_t* first_row;
   int max_chunks;
   float* o;
-  unsigned* counters;   // [batch][kv_heads]
   float* part;          // [batch][heads][max_chunks][hd + 2]: p v, then max, then sum
 };
 
-template <bool BF> __device__ inline float cval(const void* c, int64_t i) {
-  return BF ? bf16_to_f(((const uint16_t*)c)[i]) : ((const float*)c)[i];
+// the row's cache rows, kept inside the cache and the launch's chunks whatever the places say
+__device__ inline void row_range(const AttArgs& a, int b, int64_t& row0, int64_t& length) {
+  row0 = a.first_row[b];
+  row0 = row0 < 0 ? 0 : (row0 >= a.cache_len ? a.cache_len - 1 : row0);
+  length = (int64_t)a.places[b] + 1;
+  const int64_t room = a.cache_len - row0 < (int64_t)a.max_chunks * ATT_CHUNK ? a.cache_len - row0 : (int64_t)a.max_chunks * ATT_CHUNK;
+  length = length < 1 ? 1 : (length > room ? room : length);
 }
 
-// Rows first_row[b] .. first_row[b] + places[b] of kv head blockIdx.y for row b = blockIdx.z, chunk blockIdx.x of
-// ATT_CHUNK rows: wave w scores rows 64 w .. 64 w + 63 (a lane a row, its keys' loads all in flight), takes their max
-// and sum of exps, then p v with a lane on HD / 64 dimensions (the 64 rows' values loaded a row per instruction, all
-// in flight); the waves' results meet in LDS, the workgroup's goes to the workspace, and the last workgroup of the
-// row's chunks to finish combines them.
 template <int HD, bool BF>
 __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(AttArgs a) {
   constexpr int DL = HD / 64;
-  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;  // h: the query head (its key head h / rep)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rep = a.heads / a.kv_heads;
-  // the row's cache rows, kept inside the cache and the launch's chunks whatever the places say
-  int64_t row0 = a.first_row[b];
-  row0 = row0 < 0 ? 0 : (row0 >= a.cache_len ? a.cache_len - 1 : row0);
-  int64_t length = (int64_t)a.places[b] + 1;
-  const int64_t room = a.cache_len - row0 < (int64_t)a.max_chunks * ATT_CHUNK ? a.cache_len - row0 : (int64_t)a.max_chunks * ATT_CHUNK;
-  length = length < 1 ? 1 : (length > room ? room : length);
+  const int kvh = h / (a.heads / a.kv_heads);
+  int64_t row0, length;
+  row_range(a, b, row0, length);
   const int nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);
-  if (chunk >= nchunks) return;  // past the row's place: not counted
+  if (chunk >= nchunks) return;  // past the row's place
 
-  __shared__ float qs[ATT_MAX_REP][HD];
-  __shared__ float ps[ATT_WAVES][ATT_MAX_REP][64];
-  __shared__ float wm[ATT_WAVES][ATT_MAX_REP], wl[ATT_WAVES][ATT_MAX_REP];
-  __shared__ float wo[ATT_WAVES][ATT_MAX_REP][HD];
-  for (int i = tid; i < rep * HD; i += 64 * ATT_WAVES) qs[i / HD][i % HD] = a.q[((int64_t)b * a.heads + (int64_t)kvh * rep) * HD + i];
-  __syncthreads();
-
+  __shared__ float qs[HD];
+  __shared__ float ps[ATT_WAVES][64];
+  __shared__ float wm[ATT_WAVES], wl[ATT_WAVES];
+  __shared__ float wo[ATT_WAVES][HD];
   const int64_t w0 = (int64_t)chunk * ATT_CHUNK + 64 * wave;  // the wave's first row
   const int n = (int)(length - w0 < 64 ? (length - w0 > 0 ? length - w0 : 0) : 64);
-  const int64_t t = w0 + lane;
+  const int64_t t = w0 + (lane < n ? lane : (n > 0 ? n - 1 : 0));  // (a lane past the rows reads the last, unused)
   const bool valid = lane < n;
 
-  // scores
-  float s[ATT_MAX_REP];
+  // every load at once: q, the lane's row of keys, and the wave's 64 rows of values (a lane its DL dimensions)
+  float qv[(HD + 64 * ATT_WAVES - 1) / (64 * ATT_WAVES)];
 #pragma unroll
-  for (int r = 0; r < ATT_MAX_REP; ++r) s[r] = 0.f;
-  if (valid) {
-    const int64_t kb = ((int64_t)kvh * a.cache_len + row0 + t) * HD;
-    constexpr int EPL = BF ? 8 : 4;  // elements a 16-byte load
-    uint4 kw[HD / EPL];
+  for (int i = 0; i < (int)(sizeof qv / sizeof qv[0]); ++i) {
+    const int d = tid + 64 * ATT_WAVES * i;
+    qv[i] = d < HD ? a.q[((int64_t)b * a.heads + h) * HD + d] : 0.f;
+  }
+  constexpr int EPL = BF ? 8 : 4;  // elements a 16-byte load
+  uint4 kw[HD / EPL];
+  const int64_t kb = ((int64_t)kvh * a.cache_len + row0 + t) * HD;
 #pragma unroll
-    for (int i = 0; i < HD / EPL; ++i) kw[i] = *(const uint4*)((const char*)a.cache + (kb + i * EPL) * (BF ? 2 : 4));
+  for (int i = 0; i < HD / EPL; ++i) kw[i] = *(const uint4*)((const char*)a.cache + (kb + i * EPL) * (BF ? 2 : 4));
+  // values kept as loaded (bf16 pairs stay packed: half the registers) and widened when used
+  constexpr int VW = BF ? (DL + 1) / 2 : DL;  // 32-bit words a row a lane
+  uint32_t v[64][VW];
+  const int64_t vb = ((int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + w0) * HD + DL * lane;
 #pragma unroll
-    for (int i = 0; i < HD / EPL; ++i) {
-      const uint32_t w[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
-      float kv[EPL];
+  for (int tt = 0; tt < 64; ++tt) {
+    const int64_t at = vb + (int64_t)(tt < n ? tt : 0) * HD;
+    if (BF && DL == 1) v[tt][0] = ((const uint16_t*)a.cache)[at];
+    else if (BF && DL == 2) v[tt][0] = *(const uint32_t*)((const uint16_t*)a.cache + at);
+    else if (BF) { const uint2 w = *(const uint2*)((const uint16_t*)a.cache + at); v[tt][0] = w.x; v[tt][VW - 1] = w.y; }
+    else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (BF) { kv[2 * j] = bf16_to_f(w[j] & 0xFFFFu); kv[2 * j + 1] = bf16_to_f(w[j] >> 16); }
-        else kv[j] = __uint_as_float(w[j]);
-      }
-#pragma unroll
-      for (int r = 0; r < ATT_MAX_REP; ++r)
-        if (r < rep) {
-#pragma unroll
-          for (int j = 0; j < EPL; ++j) s[r] = fmaf(qs[r][i * EPL + j], kv[j], s[r]);
-        }
+      for (int i = 0; i < VW; ++i) v[tt][i] = ((const uint32_t*)a.cache)[at + i];
     }
   }
-  float mx[ATT_MAX_REP], sm[ATT_MAX_REP];
 #pragma unroll
-  for (int r = 0; r < ATT_MAX_REP; ++r) {
-    mx[r] = -INFINITY; sm[r] = 0.f;
-    if (r < rep && n > 0) {
-      const float sc = valid ? s[r] * a.scale : -INFINITY;
-      mx[r] = wave_max(sc);
-      const float p = valid ? expf(sc - mx[r]) : 0.f;
-      sm[r] = wave_sum(p);
-      ps[wave][r][lane] = p;
-    }
-  }
-  // p v: lane on dimensions DL lane .. DL lane + DL - 1, a row's values one load across the wave
-  float o[ATT_MAX_REP][DL];
-#pragma unroll
-  for (int r = 0; r < ATT_MAX_REP; ++r)
-#pragma unroll
-    for (int i = 0; i < DL; ++i) o[r][i] = 0.f;
-  if (n > 0) {
-    const int64_t vb = ((int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + w0) * HD + DL * lane;
-    float v[64][DL];
-#pragma unroll
-    for (int tt = 0; tt < 64; ++tt) {
-#pragma unroll
-      for (int i = 0; i < DL; ++i) v[tt][i] = tt < n ? cval<BF>(a.cache, vb + (int64_t)tt * HD + i) : 0.f;
-    }
-#pragma unroll
-    for (int tt = 0; tt < 64; ++tt) {
-#pragma unroll
-      for (int r = 0; r < ATT_MAX_REP; ++r)
-        if (r < rep) {
-          const float p = ps[wave][r][tt];
-#pragma unroll
-          for (int i = 0; i < DL; ++i) o[r][i] = fmaf(p, v[tt][i], o[r][i]);
-        }
-    }
-  }
-  for (int r = 0; r < rep; ++r) {
-#pragma unroll
-    for (int i = 0; i < DL; ++i) wo[wave][r][DL * lane + i] = o[r][i];
-    if (lane == 0) { wm[wave][r] = mx[r]; wl[wave][r] = sm[r]; }
+  for (int i = 0; i < (int)(sizeof qv / sizeof qv[0]); ++i) {
+    const int d = tid + 64 * ATT_WAVES * i;
+    if (d < HD) qs[d] = qv[i];
   }
   __syncthreads();
 
-  // the workgroup's waves combined: thread on (r, d) pairs
+  // the score of the lane's row: the dot with q (read from LDS, the same for every lane)
+  float s2[2] = {0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < HD / EPL; ++i) {
+    const uint32_t w[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (BF) {
+        s2[0] = fmaf(qs[i * EPL + 2 * j], __uint_as_float(w[j] << 16), s2[0]);
+        s2[1] = fmaf(qs[i * EPL + 2 * j + 1], __uint_as_float(w[j] & 0xFFFF0000u), s2[1]);
+      } else {
+        s2[j & 1] = fmaf(qs[i * EPL + j], __uint_as_float(w[j]), s2[j & 1]);
+      }
+    }
+  }
+  float mx = -INFINITY, sm = 0.f;
+  if (n > 0) {
+    const float sc = valid ? (s2[0] + s2[1]) * a.scale : -INFINITY;
+    mx = wave_max(sc);
+    const float p = valid ? expf(sc - mx) : 0.f;
+    sm = wave_sum(p);
+    ps[wave][lane] = p;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  // p v (rows past n have p = 0)
+  float o[DL];
+#pragma unroll
+  for (int i = 0; i < DL; ++i) o[i] = 0.f;
+  if (n > 0) {
+#pragma unroll
+    for (int tt = 0; tt < 64; ++tt) {
+      const float p = ps[wave][tt];
+#pragma unroll
+      for (int i = 0; i < DL; ++i) {
+        const float x = BF ? __uint_as_float(i % 2 ? v[tt][i / 2] & 0xFFFF0000u : v[tt][i / 2] << 16) : __uint_as_float(v[tt][i]);
+        o[i] = fmaf(p, x, o[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < DL; ++i) wo[wave][DL * lane + i] = o[i];
+  if (lane == 0) { wm[wave] = mx; wl[wave] = sm; }
+  __syncthreads();
+
+  // the workgroup's waves combined, a thread a dimension; o itself when the row has one chunk
   const bool alone = nchunks == 1;
-  for (int i = tid; i < rep * HD; i += 64 * ATT_WAVES) {
-    const int r = i / HD, d = i % HD;
+  for (int d = tid; d < HD; d += 64 * ATT_WAVES) {
     float big = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < ATT_WAVES; ++w) big = fmaxf(big, wm[w][r]);
+    for (int w = 0; w < ATT_WAVES; ++w) big = fmaxf(big, wm[w]);
     float num = 0.f, den = 0.f;
 #pragma unroll
     for (int w = 0; w < ATT_WAVES; ++w) {
-      if (wm[w][r] == -INFINITY) continue;  // a wave past the row's place
-      const float e = expf(wm[w][r] - big);
-      num = fmaf(e, wo[w][r][d], num);
-      den = fmaf(e, wl[w][r], den);
+      if (wm[w] == -INFINITY) continue;  // a wave past the row's place
+      const float e = expf(wm[w] - big);
+      num = fmaf(e, wo[w][d], num);
+      den = fmaf(e, wl[w], den);
     }
-    const int64_t h = (int64_t)kvh * rep + r;
     if (alone) {
       a.o[((int64_t)b * a.heads + h) * HD + d] = num / den;
     } else {
@@ -154,43 +153,42 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(AttArgs a) {
       if (d == 0) { pp[HD] = big; pp[HD + 1] = den; }
     }
   }
-  if (alone) return;
-  __threadfence();
-  __syncthreads();
-  __shared__ unsigned last;
-  if (tid == 0) last = atomicAdd(&a.counters[b * a.kv_heads + kvh], 1u) == (unsigned)(nchunks - 1);
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // the row's chunks combined by the last to finish: thread on (r, d) pairs, every chunk's loads in flight
-  for (int i = tid; i < rep * HD; i += 64 * ATT_WAVES) {
-    const int r = i / HD, d = i % HD;
-    const float* pp = a.part + (((int64_t)b * a.heads + (int64_t)kvh * rep + r) * a.max_chunks) * (HD + 2);
-    float big = -INFINITY;
-    for (int c = 0; c < nchunks; ++c) big = fmaxf(big, pp[c * (HD + 2) + HD]);
-    float num = 0.f, den = 0.f;
-    for (int c0 = 0; c0 < nchunks; c0 += 8) {
-      float m8[8], l8[8], v8[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const bool ok = c0 + j < nchunks;
-        const float* q = pp + (int64_t)(c0 + j) * (HD + 2);
-        m8[j] = ok ? q[HD] : -INFINITY; l8[j] = ok ? q[HD + 1] : 0.f; v8[j] = ok ? q[d] : 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (m8[j] == -INFINITY) continue;
-        const float e = expf(m8[j] - big);
-        num = fmaf(e, v8[j], num);
-        den = fmaf(e, l8[j], den);
-      }
-    }
-    a.o[((int64_t)b * a.heads + (int64_t)kvh * rep + r) * HD + d] = num / den;
-  }
-  if (tid == 0) atomicExch(&a.counters[b * a.kv_heads + kvh], 0u);  // ready for the next call
 }
 
-static size_t counter_bytes(int batch, int heads) { return ((size_t)batch * heads * sizeof(unsigned) + 255) / 256 * 256; }
+// the chunks of row blockIdx.y, head blockIdx.x combined: a thread a dimension, every chunk's loads in flight
+template <int HD>
+__global__ __launch_bounds__(HD) void attention_combine(AttArgs a) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  int64_t row0, length;
+  row_range(a, b, row0, length);
+  const int nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);
+  if (nchunks == 1) return;  // the first kernel wrote o
+  const float* pp = a.part + ((int64_t)b * a.heads + h) * a.max_chunks * (HD + 2);
+  float big = -INFINITY, num = 0.f, den = 0.f;
+  for (int c0 = 0; c0 < nchunks; c0 += 16) {  // 16 chunks' loads at once, the running sums rescaled to a new largest
+    float m16[16], l16[16], v16[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bool ok = c0 + j < nchunks;
+      const float* q = pp + (int64_t)(ok ? c0 + j : c0) * (HD + 2);
+      m16[j] = ok ? q[HD] : -INFINITY; l16[j] = q[HD + 1]; v16[j] = q[d];
+    }
+    float top = big;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) top = fmaxf(top, m16[j]);
+    if (big != -INFINITY) { const float f = expf(big - top); num *= f; den *= f; }
+    big = top;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (m16[j] == -INFINITY) continue;
+      const float e = expf(m16[j] - big);
+      num = fmaf(e, v16[j], num);
+      den = fmaf(e, l16[j], den);
+    }
+  }
+  a.o[((int64_t)b * a.heads + h) * HD + d] = num / den;
+}
+
 
 }  // namespace fh
 
@@ -199,15 +197,15 @@ using namespace fh;
 extern "C" size_t fh_attention_workspace_bytes(int batch, int heads, int head_dim, int64_t max_context) {
   if (batch < 1 || heads < 1 || head_dim < 1 || max_context < 1) return 0;
   const int64_t chunks = (max_context + ATT_CHUNK - 1) / ATT_CHUNK;
-  return counter_bytes(batch, heads) + (size_t)batch * heads * chunks * (head_dim + 2) * sizeof(float);
+  return (size_t)batch * heads * chunks * (head_dim + 2) * sizeof(float);
 }
 
 extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch,
                                    int heads, int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row,
                                    int64_t max_context, float* o, void* workspace, size_t ws_bytes, void* stream) {
   if (!q || !cache || !places || !first_row || !o) return fail(FH_EINVAL, "fh_attention_decode: null pointer");
-  if (batch < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads || heads / kv_heads > ATT_MAX_REP)
-    return fail(FH_EINVAL, "fh_attention_decode: heads must be a multiple of kv_heads, at most 8 query heads a key head");
+  if (batch < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads)
+    return fail(FH_EINVAL, "fh_attention_decode: heads must be a multiple of kv_heads");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(FH_EUNSUP, "fh_attention_decode: head_dim 64, 128 or 256");
   if (cache_dtype != FH_F32 && cache_dtype != FH_BF16) return fail(FH_EUNSUP, "fh_attention_decode: cache is FH_F32 or FH_BF16");
   if (max_context < 1 || max_context > cache_len) return fail(FH_EINVAL, "fh_attention_decode: max_context outside 1..cache_len");
@@ -220,15 +218,18 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   a.places = places; a.first_row = first_row;
   a.max_chunks = (int)((max_context + ATT_CHUNK - 1) / ATT_CHUNK);
   a.o = o;
-  a.counters = (unsigned*)workspace;
-  a.part = workspace ? (float*)((char*)workspace + counter_bytes(batch, heads)) : nullptr;
-  dim3 grid(a.max_chunks, kv_heads, batch), block(64 * ATT_WAVES);
+  a.part = (float*)workspace;
+  dim3 grid(a.max_chunks, heads, batch), block(64 * ATT_WAVES);
   hipStream_t s = as_stream(stream);
   const bool bf = cache_dtype == FH_BF16;
+  const dim3 cgrid(heads, batch);
   switch (head_dim) {
-    case 64: if (bf) hipLaunchKernelGGL((attention_kernel<64, true>), grid, block, 0, s, a); else hipLaunchKernelGGL((attention_kernel<64, false>), grid, block, 0, s, a); break;
-    case 128: if (bf) hipLaunchKernelGGL((attention_kernel<128, true>), grid, block, 0, s, a); else hipLaunchKernelGGL((attention_kernel<128, false>), grid, block, 0, s, a); break;
-    default: if (bf) hipLaunchKernelGGL((attention_kernel<256, true>), grid, block, 0, s, a); else hipLaunchKernelGGL((attention_kernel<256, false>), grid, block, 0, s, a); break;
+    case 64: if (bf) hipLaunchKernelGGL((attention_kernel<64, true>), grid, block, 0, s, a); else hipLaunchKernelGGL((attention_kernel<64, false>), grid, block, 0, s, a);
+             if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<64>, cgrid, dim3(64), 0, s, a); break;
+    case 128: if (bf) hipLaunchKernelGGL((attention_kernel<128, true>), grid, block, 0, s, a); else hipLaunchKernelGGL((attention_kernel<128, false>), grid, block, 0, s, a);
+              if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<128>, cgrid, dim3(128), 0, s, a); break;
+    default: if (bf) hipLaunchKernelGGL((attention_kernel<256, true>), grid, block, 0, s, a); else hipLaunchKernelGGL((attention_kernel<256, false>), grid, block, 0, s, a);
+             if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<256>, cgrid, dim3(256), 0, s, a); break;
   }
   return check_launch("fh_attention_decode");
 }

@@ -229,3 +229,36 @@ extern "C" int fh_argmax_rows(const float* x, int64_t rows, int64_t n, int32_t* 
   hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(1024), 0, as_stream(stream), x, n, ids);
   return check_launch("fh_argmax_rows");
 }
+
+// ---- argmax from the GEMV's per-run pairs: one workgroup a row ---------------------------------------------------
+__global__ __launch_bounds__(256) void argmax_parts_kernel(const int2* __restrict__ parts, int64_t n, int32_t* __restrict__ ids) {
+  const int2* row = parts + (int64_t)blockIdx.x * n;
+  float best = -INFINITY;
+  int at = INT32_MAX;
+  for (int64_t c = threadIdx.x; c < n; c += blockDim.x) {
+    const int2 p = row[c];
+    const float v = __int_as_float(p.x);
+    if (v > best || (v == best && p.y < at)) { best = v; at = p.y; }
+  }
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(best, m, 64);
+    const int oa = __shfl_xor(at, m, 64);
+    if (ov > best || (ov == best && oa < at)) { best = ov; at = oa; }
+  }
+  __shared__ float bv[4];
+  __shared__ int ba[4];
+  const int w = threadIdx.x / 64;
+  if ((threadIdx.x & 63) == 0) { bv[w] = best; ba[w] = at; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 4; ++i)
+      if (bv[i] > best || (bv[i] == best && ba[i] < at)) { best = bv[i]; at = ba[i]; }
+    ids[blockIdx.x] = at == INT32_MAX ? 0 : at;
+  }
+}
+
+extern "C" int fh_argmax_parts(const void* parts, int64_t rows, int64_t nparts, int32_t* ids, void* stream) {
+  if (!parts || !ids || rows <= 0 || nparts <= 0) return fail(FH_EINVAL, "fh_argmax_parts: bad arguments");
+  hipLaunchKernelGGL(argmax_parts_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), (const int2*)parts, nparts, ids);
+  return check_launch("fh_argmax_parts");
+}

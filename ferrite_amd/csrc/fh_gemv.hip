@@ -31,6 +31,7 @@ struct GemvArgs {
   int heads, kv_heads, head_dim;
   const float* cos_tab; const float* sin_tab; const int32_t* places; const int32_t* cache_rows;
   void* cache; int cache_bf16; int64_t cache_len;
+  int2* argmax_parts;
 };
 
 __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
@@ -60,14 +61,16 @@ __device__ inline void magnitudes(const uint2& m, float (&f)[16]) {
   }
 }
 
-// rows a lane has in flight at once, by format and batch rows (about 4 KiB of weight a wave for one batch row)
-__host__ __device__ constexpr int gemv_group(bool four, int b) { return (b <= 2 ? 4 : b <= 4 ? 2 : 1) * (four ? 2 : 1); }
+// rows a lane has in flight at once, by format, batch rows and runs (about 4 KiB of weight a wave at batch 1)
+__host__ __device__ constexpr int gemv_group(bool four, int b, int p) {
+  return (b <= 2 ? 4 : b <= 4 ? 2 : 1) * (four ? 2 : 1) / p > 0 ? (b <= 2 ? 4 : b <= 4 ? 2 : 1) * (four ? 2 : 1) / p : 1;
+}
 
 template <bool FOUR, int B, int P, bool NORM>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   constexpr int V = B * P * 16;       // a lane's partial sums: [b][p][j]
   constexpr int G = B * P;
-  constexpr int U = gemv_group(FOUR, B);
+  constexpr int U = gemv_group(FOUR, B, P);
   constexpr int RB = FOUR ? 8 : 16;   // bytes of a run's row
   using Row = typename std::conditional<FOUR, uint2, uint4>::type;
   const int lane = threadIdx.x & 63;
@@ -177,6 +180,17 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
         s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
         if (j == 0) a.ssq_out[(int64_t)b * (a.N / 16) + nb[p]] = s;
       }
+      if (kind == FH_EP_STORE && a.argmax_parts) {  // the run's largest and its first column
+        float bv = v;
+        int bc = (int)col;
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1) {
+          const float ov = __shfl_xor(bv, m, 64);
+          const int oc = __shfl_xor(bc, m, 64);
+          if (ov > bv || (ov == bv && oc < bc)) { bv = ov; bc = oc; }
+        }
+        if (j == 0) a.argmax_parts[(int64_t)b * (a.N / 16) + nb[p]] = make_int2(__float_as_int(bv), bc);
+      }
     }
   } else if (P == 2 && kind == FH_EP_SILU_GATE) {
     for (int i = lane; i < B * 16; i += 64) {
@@ -252,7 +266,7 @@ static Plan plan(int64_t K, int64_t N, int fmt, int kind, int batch) {
   p.most = p.P == 1 ? 8 : 4;
   p.items = (int)(N / 16 / p.P);
   const int b = batch < p.most ? batch : p.most;
-  const int unit = 64 * gemv_group(fmt == FH_BFP4, b);
+  const int unit = 64 * gemv_group(fmt == FH_BFP4, b, p.P);
   const int64_t units = (K + unit - 1) / unit;
   int64_t W = 1;
   while (W < 16 && W * p.items < 16384) W *= 2;
@@ -290,7 +304,7 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
       a.norm_w = ep->norm_w; a.ssq_in = ep->ssq_in; a.ssq_parts = (int)(K / 16); a.eps = ep->eps; a.centered = ep->centered;
     }
     switch (ep->kind) {
-      case FH_EP_STORE: break;
+      case FH_EP_STORE: a.argmax_parts = (int2*)ep->argmax_parts; break;
       case FH_EP_RESIDUAL:
         if (!ep->residual) return fail(FH_EINVAL, "fh_gemv_bfp: FH_EP_RESIDUAL needs residual");
         a.residual = ep->residual; a.ssq_out = ep->ssq_out;
@@ -331,6 +345,7 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
     if (c.residual) c.residual += (int64_t)b0 * ldy;
     if (c.ssq_out) c.ssq_out += (int64_t)b0 * (N / 16);
     if (c.places) { c.places += b0; c.cache_rows += b0; }
+    if (c.argmax_parts) c.argmax_parts += (int64_t)b0 * (N / 16);
     int rc = p.P == 1 ? (four ? dispatch_batch<true, 1>(c, n, p.items, p.W, s) : dispatch_batch<false, 1>(c, n, p.items, p.W, s))
                       : (four ? dispatch_batch<true, 2>(c, n, p.items, p.W, s) : dispatch_batch<false, 2>(c, n, p.items, p.W, s));
     if (rc) return rc;

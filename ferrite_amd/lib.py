@@ -24,7 +24,7 @@ class Epilogue(ctypes.Structure):
   _fields_ = [("kind", I), ("norm_w", P), ("ssq_in", P), ("eps", ctypes.c_float), ("centered", I),
               ("residual", P), ("ssq_out", P), ("split", I), ("heads", I), ("kv_heads", I), ("head_dim", I),
               ("cos_tab", P), ("sin_tab", P), ("places", P), ("cache_rows", P), ("cache", P), ("cache_dtype", I),
-              ("cache_len", L)]
+              ("cache_len", L), ("argmax_parts", P)]
 
 
 SIGNATURES = {
@@ -38,6 +38,7 @@ SIGNATURES = {
   "fh_attention_workspace_bytes": ([I, I, I, L], S),
   "fh_attention_decode": ([P, P, I, L, I, I, I, I, P, P, L, P, P, S, P], I),
   "fh_argmax_rows": ([P, L, L, P, P], I),
+  "fh_argmax_parts": ([P, L, L, P, P], I),
 }
 
 _lib = None

@@ -112,6 +112,7 @@ class Decoder:
     self.h = z(B, c.ffn)
     self.logits = z(B, c.vocab)
     self.picks = torch.zeros(B, dtype=torch.int32, device=self.device)
+    self.parts = torch.zeros(B, c.vocab // 16, dtype=torch.int64, device=self.device)  # each run of 16 logits' best
     self.ws = ops.attention_workspace(B, c.heads, hd, context, self.device)
     self.graph = None
 
@@ -145,9 +146,9 @@ class Decoder:
       ops.gemv(self.x, L.gate_up, ep, out=self.h)
       ep = ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq)
       ops.gemv(self.h, L.down, ep, out=self.x)
-    ep = ops.epilogue(lib.EP_STORE, norm_w=self.norm, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered))
+    ep = ops.epilogue(lib.EP_STORE, norm_w=self.norm, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered), argmax_parts=self.parts)
     ops.gemv(self.x, self.head, ep, out=self.logits)
-    ops.argmax_rows(self.logits, self.picks)
+    ops.argmax_parts(self.parts, self.picks)
 
   def step(self, ids=None, places=None, slots=None, replay=True):
     """One step: the logits (fp32, [batch][vocab]) and picks for tokens ids at places. With replay, the step runs as

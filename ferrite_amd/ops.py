@@ -119,3 +119,11 @@ def argmax_rows(x, ids=None):
   if ids is None: ids = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)
   lib.call("fh_argmax_rows", _ptr(x), x.shape[0], x.shape[1], _ptr(ids), _stream())
   return ids
+
+
+def argmax_parts(parts, ids=None):
+  """Each row's argmax from the (value, column) pairs a GEMV epilogue left (fh_argmax_parts). parts: int64 [rows][n]."""
+  _dev(parts)
+  if ids is None: ids = torch.empty(parts.shape[0], dtype=torch.int32, device=parts.device)
+  lib.call("fh_argmax_parts", _ptr(parts), parts.shape[0], parts.shape[1], _ptr(ids), _stream())
+  return ids

@@ -102,6 +102,9 @@ typedef struct fh_epilogue {
   void* cache;              /* [2*kv_heads][cache_len][head_dim]: keys' heads then values', fp32 or bf16 */
   int cache_dtype;
   int64_t cache_len;
+  /* FH_EP_STORE: each row's largest value of each run of 16 columns and its column (the first of equals), as
+   * (float, int32) pairs [batch][N/16], for fh_argmax_parts: greedy decoding's pick without a second pass over y */
+  void* argmax_parts;
 } fh_epilogue;
 
 /* y (dtype y_dtype, row stride ldy) from x @ W and the epilogue. x: fp32. w_mant/w_exps: a packed [K][N] weight
@@ -131,6 +134,9 @@ int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int6
 /* For each row of x[rows][n] (fp32), its largest value's column (the first of equals), into ids[rows]: greedy
  * decoding's pick (models/llama.py:792, numpy's argmax). */
 int fh_argmax_rows(const float* x, int64_t rows, int64_t n, int32_t* ids, void* stream);
+
+/* The same pick from the (value, column) pairs an FH_EP_STORE epilogue left in argmax_parts: parts [rows][nparts]. */
+int fh_argmax_parts(const void* parts, int64_t rows, int64_t nparts, int32_t* ids, void* stream);
 
 #ifdef __cplusplus
 }

@@ -234,3 +234,12 @@ def test_embed_and_argmax(cuda):
   v[1, 7] = v[1, 70] = v[1].max() + 1  # a tie: the first
   v[2, :] = 0
   assert ops().argmax_rows(to_gpu(v)).cpu().numpy().tolist() == np.argmax(v, 1).tolist()
+  # the same picks from a GEMV epilogue's per-run pairs: y = x @ I holds x, ties included
+  from ferrite_amd import lib as L
+  x = v[:, :4096].copy()
+  x[0, 100] = x[0, 3000] = x[0].max() + 1
+  eye = ops().pack(to_gpu(np.eye(4096, dtype=np.float32)))
+  parts = torch.zeros(3, 4096 // 16, dtype=torch.int64, device="cuda")
+  y = ops().gemv(to_gpu(x), eye, ops().epilogue(L.EP_STORE, argmax_parts=parts))
+  assert np.array_equal(y.cpu().numpy(), x)
+  assert ops().argmax_parts(parts).cpu().numpy().tolist() == np.argmax(x, 1).tolist()
