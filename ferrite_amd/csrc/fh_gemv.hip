@@ -61,10 +61,8 @@ __device__ inline void magnitudes(const uint2& m, float (&f)[16]) {
   }
 }
 
-// rows a lane has in flight at once, by format, batch rows and runs (about 4 KiB of weight a wave at batch 1)
-__host__ __device__ constexpr int gemv_group(bool four, int b, int p) {
-  return (b <= 2 ? 4 : b <= 4 ? 2 : 1) * (four ? 2 : 1) / p > 0 ? (b <= 2 ? 4 : b <= 4 ? 2 : 1) * (four ? 2 : 1) / p : 1;
-}
+// rows a lane has in flight at once, by format and batch rows (about 4 KiB of weight a wave and run at batch 1)
+__host__ __device__ constexpr int gemv_group(bool four, int b, int p) { return (b <= 2 ? 4 : b <= 4 ? 2 : 1) * (four ? 2 : 1) + 0 * p; }
 
 template <bool FOUR, int B, int P, bool NORM>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
@@ -91,6 +89,23 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.f;
+
+  // what wave 0's epilogue reads, loaded now so that the loads overlap the stream: the sums of squares (up to 256
+  // runs a row, K <= 4096; a longer row is read at the end) and each row's place
+  constexpr int PRE = 4;
+  float ssq_pre[B][PRE];
+  int place_pre[B];
+  if (slice == 0) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+#pragma unroll
+      for (int i = 0; i < PRE; ++i) {
+        const int at = lane + 64 * i;
+        ssq_pre[b][i] = (NORM && a.ssq_parts <= 64 * PRE && at < a.ssq_parts) ? a.ssq_in[(int64_t)b * a.ssq_parts + at] : 0.f;
+      }
+      place_pre[b] = a.places ? a.places[b] : 0;
+    }
+  }
 
   // U rows of each run, 64 apart, a lane; rows past r1 are read at r1 - 1 (they exist) and count as 0
   for (int k0 = r0; k0 < r1; k0 += 64 * U) {
@@ -158,7 +173,12 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     rs[b] = 1.f;
     if (NORM) {
       float s = 0.f;
-      for (int i = lane; i < a.ssq_parts; i += 64) s += a.ssq_in[(int64_t)b * a.ssq_parts + i];
+      if (a.ssq_parts <= 64 * PRE) {
+#pragma unroll
+        for (int i = 0; i < PRE; ++i) s += ssq_pre[b][i];
+      } else {
+        for (int i = lane; i < a.ssq_parts; i += 64) s += a.ssq_in[(int64_t)b * a.ssq_parts + i];
+      }
       s = wave_sum(s);
       rs[b] = 1.0f / sqrtf(s / (float)K + a.eps);
     }
@@ -207,7 +227,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
       const float r = NORM ? rs[b] : 1.f;
       float x0 = fin[(b * P) * 16 + j] * r, x1 = fin[(b * P + 1) * 16 + j] * r;
-      const int place = a.places[b];
+      int place = place_pre[0];
+#pragma unroll
+      for (int q = 1; q < B; ++q) if (b == q) place = place_pre[q];
       if (h < a.heads + a.kv_heads) {  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
         const float* cs = a.cos_tab + (int64_t)place * hd;
         const float* sn = a.sin_tab + (int64_t)place * hd;
