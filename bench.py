@@ -1,4 +1,4 @@
-"""The hot path's benchmark: ferrite's block-float decode on one MI355X, on BASELINE config 3 (Llama-3.1-8B's shape,
+"""The hot path's benchmark: ferrite's block-float decode on one MI355X, on the 8B decode workload (Llama-3.1-8B's shape,
 attention and the output layer in bfp8, every MLP matrix in bfp4, a bf16 KV cache at context 2048, batch 1).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c3-bfp8|c2] [--batch B] [--no-cpu]
@@ -50,22 +50,34 @@ def timed_graph(fn, reps, stream):
 
 
 def gemv_rates(dec, stream, reps=5):
-  """Each GEMV of the step, launched back to back over every block's weight (so each launch reads a matrix the last
-  ones did not: 32 distinct matrices, past the 256 MB Infinity Cache), in a graph timed by events: (name, fmt, bytes a
-  launch, us a launch, GB/s)."""
+  """Each GEMV of the step exactly as the step launches it (its epilogue and prologue included), back to back over
+  every block's weight (32 distinct matrices, past the 256 MB Infinity Cache), in a graph timed by HIP events on the
+  stream the kernels run on: {name: (fmt, K, N, bytes a launch, us a launch, GB/s)}. Bytes are the algorithmic ones:
+  the packed weight, x and the norm's weights read once, y written once."""
   from ferrite_amd import lib, ops
-  c = dec.c
-  x = torch.randn(dec.batch, max(c.dim, c.ffn, c.heads * dec.hd), device=dec.device)
+  c, B = dec.c, dec.batch
+  cache_dtype = lib.DTYPES["bf16" if dec.kv_dtype == torch.bfloat16 else "fp32"]
+  calls = {
+    "qkv": [(dec.x, L.qkv, lambda L=L, l=l: ops.epilogue(lib.EP_ROPE_KV, norm_w=L.norm1, ssq_in=dec.ssq, eps=c.eps, heads=c.heads,
+             kv_heads=c.kv, head_dim=dec.hd, cos_tab=dec.cos, sin_tab=dec.sin, places=dec.places, cache_rows=dec.rows,
+             cache=dec.cache[l], cache_dtype=cache_dtype, cache_len=dec.cache[l].shape[1]), dec.q, c.dim * 4)
+            for l, L in enumerate(dec.layers)],
+    "o": [(dec.att, L.o, lambda: ops.epilogue(lib.EP_RESIDUAL, residual=dec.x, ssq_out=dec.ssq), dec.x, 0) for L in dec.layers],
+    "gate_up": [(dec.x, L.gate_up, lambda L=L: ops.epilogue(lib.EP_SILU_GATE, norm_w=L.norm2, ssq_in=dec.ssq, eps=c.eps, split=c.ffn),
+                 dec.h, c.dim * 4) for L in dec.layers],
+    "down": [(dec.h, L.down, lambda: ops.epilogue(lib.EP_RESIDUAL, residual=dec.x, ssq_out=dec.ssq), dec.x, 0) for L in dec.layers],
+    "head": [(dec.x, dec.head, lambda: ops.epilogue(lib.EP_STORE, norm_w=dec.norm, ssq_in=dec.ssq, eps=c.eps, argmax_parts=dec.parts),
+              dec.logits, c.dim * 4)] * 4,
+  }
   out = {}
-  for name in ("qkv", "o", "gate_up", "down", "head"):
-    ws = [getattr(L, name) for L in dec.layers] if name != "head" else [dec.head] * 4
-    y = torch.empty(dec.batch, max(w.N for w in ws), device=dec.device)
+  for name, seq in calls.items():
+    eps = [(x, w, make(), y, extra) for x, w, make, y, extra in seq]  # built once, outside the capture
     def run():
-      for w in ws: ops.gemv(x[:, :w.K], w, out=y[:, :w.N])
+      for x, w, ep, y, extra in eps: ops.gemv(x, w, ep, out=y)
     ms = timed_graph(run, reps, stream)
-    per = ms / len(ws) * 1e-3
-    w = ws[0]
-    nbytes = w.nbytes + dec.batch * (w.K + w.N) * 4  # W + x + y, each read or written once
+    per = ms / len(eps) * 1e-3
+    x, w, ep, y, extra = eps[0]
+    nbytes = w.nbytes + B * w.K * 4 + B * y.shape[1] * 4 + extra  # W, x, y (and the norm's weights)
     out[name] = dict(fmt=w.fmt, K=w.K, N=w.N, bytes=nbytes, us=per * 1e6, gbs=nbytes / per / 1e9)
   return out
 
@@ -120,7 +132,7 @@ def main():
   ap.add_argument("--no-cpu", action="store_true")
   args = ap.parse_args()
   if args.gpus != 1:
-    print("bench.py measures one GPU: this build has no multi-GPU path (the decode would shard by columns, as DESIGN.md says)",
+    print("bench.py measures one GPU: this build has no multi-GPU path (a decode would shard each weight by columns)",
           file=sys.stderr)
     raise SystemExit(2)
   from ferrite_amd import lib
@@ -156,8 +168,9 @@ def main():
   rates = gemv_rates(dec, stream)
   for k, r in rates.items():
     print(f"# gemv {k:8s} {r['fmt']} {r['K']}x{r['N']}: {r['us']:.2f} us, {r['gbs']:.0f} GB/s ({r['gbs'] * 1e9 / HBM_PEAK:.1%})", file=sys.stderr, flush=True)
-  dom = max(rates, key=lambda k: rates[k]["bytes"] * (c.layers if k != "head" else 1))
+  dom = max(rates, key=lambda k: rates[k]["us"] * (c.layers if k != "head" else 1))  # the most time in a step
   r = rates[dom]
+  epi = {"qkv": "RMSNorm+RoPE+KV put", "o": "residual", "gate_up": "RMSNorm+SiLU*gate", "down": "residual", "head": "RMSNorm+argmax"}
   cpu = None
   if not args.no_cpu:
     cpu = cpu_baseline(c, mode, context)
@@ -168,11 +181,11 @@ def main():
     "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
     "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
     "dtype": "bfp8/bfp4 weights, fp32 math", "data": "synthetic (random-init weights, random bf16 KV cache)",
-    "config": {"workload": f"BASELINE config 3: Llama-3.1-8B-shape decode, batch {B}, context {context}, "
+    "config": {"workload": f"config 3: Llama-3.1-8B-shape decode, batch {B}, context {context}, "
                            f"{'attention+head bfp8, MLP bfp4' if mode == 'experts' else 'all bfp8'}, bf16 KV",
                "global_batch": B, "seq_len": context, "parallelism": "none (1 GPU)"},
     "step_gbs": round(step_bytes / ms / 1e6, 1), "step_bytes": step_bytes,
-    "roofline": {"bound": "hbm", "kernel": f"gemv {dom} ({r['fmt']} {r['K']}x{r['N']})", "achieved": round(r["gbs"], 1),
+    "roofline": {"bound": "hbm", "kernel": f"gemv {dom} + {epi[dom]} ({r['fmt']} {r['K']}x{r['N']})", "achieved": round(r["gbs"], 1),
                  "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(r["gbs"] * 1e9 / HBM_PEAK, 4), "traffic": None},
     "gemv_gbs": {k: round(v["gbs"], 1) for k, v in rates.items()},
     "gemv_us": {k: round(v["us"], 3) for k, v in rates.items()},

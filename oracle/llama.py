@@ -247,13 +247,13 @@ def random_weights(c, rng, sd=0.02, norm_sd=0.1, embed_sd=1.0):
 
 
 def smollm(layers=30, vocab=49152, places=256):
-  """SmolLM-135M's shape: 576 wide, 9 query heads sharing 3 key heads of 64, MLP 1536, RMSNorm eps
+  """SmolLM-135M's shape (benchmark config 2): 576 wide, 9 query heads sharing 3 key heads of 64, MLP 1536, RMSNorm eps
   1e-5, RoPE theta 10000, the output layer the embedding (tied)."""
   return model(dim=576, heads=9, kv=3, layers=layers, eps=1e-5, theta=10000.0, vocab=vocab, ffn=1536, places=places, tied=True)
 
 
 def llama8b(layers=32, vocab=128256, places=2048, rope=True):
-  """Llama-3.1-8B's shape: 4096 wide, 32 query heads sharing 8 key heads of 128, MLP 14336, vocab
+  """Llama-3.1-8B's shape (benchmark config 3): 4096 wide, 32 query heads sharing 8 key heads of 128, MLP 14336, vocab
   128256, theta 500000 with Llama 3's RoPE scaling (test_sim.py:1933-1934), its own output layer."""
   r = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
   return model(dim=4096, heads=32, kv=8, layers=layers, eps=1e-5, theta=500000.0, vocab=vocab, ffn=14336, places=places,

@@ -1,6 +1,6 @@
 """Parity of the HIP kernels with the CPU oracle on the same seeded inputs, through the C-ABI (ferrite_amd.ops calls
 libferrite_hip.so): packing and unpacking bit for bit, the GEMV and each epilogue within fp32 summation's error, decode
-attention. Sizes are those the oracle finishes in seconds; BASELINE's shapes appear as properties where numpy would be
+attention. Sizes are those the oracle finishes in seconds; the benchmark's shapes appear as properties where numpy would be
 slow. The reference's own tests of the same path: test_bfp (test/test_sim.py:371-388), test_matmul_random (325-335),
 test_matmul_exact (310-323), test_block_float_cache (2081-2107)."""
 import math
@@ -98,7 +98,7 @@ def check_close(got, want, bound, what):
 
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
 def test_gemv_config1(cuda, fmt):
-  # x[1,576] bf16 ~N(0,1), W[576,1536] ~N(0,0.02) fp32 packed (16 along N, ferrite's), y fp32
+  # benchmark config 1: x[1,576] bf16 ~N(0,1), W[576,1536] ~N(0,0.02) fp32 packed (16 along N, ferrite's), y fp32
   rng = np.random.default_rng(0)
   x = O.bf16(rng.normal(0, 1, (1, 576)))
   w = rng.normal(0, 0.02, (576, 1536)).astype(np.float32)

@@ -82,7 +82,7 @@ def test_replay_is_the_step(cuda):
 
 
 def test_config2_smollm_32_greedy_tokens(cuda):
-  # SmolLM-135M's shape, 30 blocks, vocab 49152, bfp8 weights N(0, 0.02), a bf16 KV cache
+  # benchmark config 2: SmolLM-135M's shape, 30 blocks, vocab 49152, bfp8 weights N(0, 0.02), a bf16 KV cache
   # prefilled from a 128-token seeded prompt, then 32 greedy steps: the same 32 tokens as numpy
   rng = np.random.default_rng(2)
   c = smol(30, 49152, places=256)
