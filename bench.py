@@ -82,6 +82,17 @@ def gemv_rates(dec, stream, reps=5):
   return out
 
 
+def measured_traffic(kernel, config, batch):
+  """HBM bytes a launch of `kernel` moves, as the committed rocprofv3 counter summaries under profiles/ record them
+  (lines `traffic: <kernel> <config> b<batch> <bytes>`: FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's
+  reading for a copy kernel of known size in the same run), or None when no summary covers it."""
+  import glob, re
+  for f in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+    for m in re.finditer(r"^traffic: (\S+) (\S+) b(\d+) (\d+)$", open(f).read(), re.M):
+      if (m[1], m[2], int(m[3])) == (kernel, config, batch): return int(m[4])
+  return None
+
+
 def cpu_baseline(c, mode, context, layers_timed=1):
   """The numpy restatement (oracle/llama.py) of one decode token on this host: one block at the step's context plus the
   output layer, each the median of 3 timed runs after a warm-up, the block's time scaled by c.layers. Float64 caches,
@@ -130,6 +141,9 @@ def main():
   ap.add_argument("--config", default="c3")
   ap.add_argument("--batch", type=int, default=1)
   ap.add_argument("--no-cpu", action="store_true")
+  ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                  help="first run a plain copy kernel (torch.neg) over MIB MiB: the known-size kernel that calibrates "
+                       "rocprofv3's FETCH_SIZE/WRITE_SIZE counters in the same run")
   args = ap.parse_args()
   if args.gpus != 1:
     print("bench.py measures one GPU: this build has no multi-GPU path (a decode would shard each weight by columns)",
@@ -139,6 +153,12 @@ def main():
   from ferrite_amd import llama as G
   lib.load()
   dev = torch.device("cuda:0")
+  if args.copy_probe:
+    src = torch.ones(args.copy_probe << 18, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2): torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
   c, mode, context = config(args.config)
   t0 = time.time()
   dec = G.Decoder(c, G.random_weights(c, seed=1, device=dev), mode=mode, kv="bf16", batch=args.batch, context=context,
@@ -186,7 +206,8 @@ def main():
                "global_batch": B, "seq_len": context, "parallelism": "none (1 GPU)"},
     "step_gbs": round(step_bytes / ms / 1e6, 1), "step_bytes": step_bytes,
     "roofline": {"bound": "hbm", "kernel": f"gemv {dom} + {epi[dom]} ({r['fmt']} {r['K']}x{r['N']})", "achieved": round(r["gbs"], 1),
-                 "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(r["gbs"] * 1e9 / HBM_PEAK, 4), "traffic": None},
+                 "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(r["gbs"] * 1e9 / HBM_PEAK, 4),
+                 "traffic": measured_traffic(dom, args.config, B)},
     "gemv_gbs": {k: round(v["gbs"], 1) for k, v in rates.items()},
     "gemv_us": {k: round(v["us"], 3) for k, v in rates.items()},
     "cpu_baseline": cpu,
