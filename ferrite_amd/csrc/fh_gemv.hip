@@ -12,60 +12,15 @@
 // latency-bound stream, and that is what hides the latency. Nothing crosses workgroups: no atomics, no fences.
 #include <math.h>
 #include <type_traits>
-#include "fh_common.h"
+#include "fh_epilogue.h"
 
 namespace fh {
-
-struct GemvArgs {
-  const void* x; int64_t ldx;
-  const uint8_t* mant; const uint8_t* exps; int64_t K; int64_t N;
-  int pair_half;            // P == 2: the runs of a pair are nb0 and nb0 + pair_half
-  int rows;                 // K in slices of `rows` rows (a multiple of 64), one a wave
-  // prologue
-  const float* norm_w; const float* ssq_in; int ssq_parts; float eps; int centered;
-  // epilogue
-  int kind;
-  void* y; int64_t ldy; int y_bf16;
-  const float* residual; float* ssq_out;
-  int split;
-  int heads, kv_heads, head_dim;
-  const float* cos_tab; const float* sin_tab; const int32_t* places; const int32_t* cache_rows;
-  void* cache; int cache_bf16; int64_t cache_len;
-  int2* argmax_parts;
-};
-
-__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
-
-__device__ inline void store_out(void* y, int bf16, int64_t at, float v) {
-  if (bf16) ((uint16_t*)y)[at] = (uint16_t)bf16_rne_f(v);
-  else ((float*)y)[at] = v;
-}
-
-// the 16 magnitudes of a run's row as floats: bfp8's 16 bytes are the signed q; bfp4's 8 bytes give 16 q (the 16 is
-// folded into the scale: q * 2^(e - 129) = 16 q * 2^(e - 133))
-__device__ inline void magnitudes(const uint4& m, float (&f)[16]) {
-  const uint32_t w[4] = {m.x, m.y, m.z, m.w};
-#pragma unroll
-  for (int j = 0; j < 16; ++j) f[j] = (float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 255u);
-}
-__device__ inline void magnitudes(const uint2& m, float (&f)[16]) {
-  const uint32_t w[2] = {m.x, m.y};
-#pragma unroll
-  for (int d = 0; d < 2; ++d) {
-    const uint32_t hi = w[d] & 0xF0F0F0F0u, lo = (w[d] << 4) & 0xF0F0F0F0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[8 * d + 2 * i] = (float)(int8_t)((lo >> (8 * i)) & 255u);
-      f[8 * d + 2 * i + 1] = (float)(int8_t)((hi >> (8 * i)) & 255u);
-    }
-  }
-}
 
 // rows a lane has in flight at once, by format and batch rows (about 4 KiB of weight a wave and run at batch 1)
 __host__ __device__ constexpr int gemv_group(bool four, int b, int p) { return (b <= 2 ? 4 : b <= 4 ? 2 : 1) * (four ? 2 : 1) + 0 * p; }
 
 template <bool FOUR, int B, int P, bool NORM>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
   constexpr int V = B * P * 16;       // a lane's partial sums: [b][p][j]
   constexpr int G = B * P;
   constexpr int U = gemv_group(FOUR, B, P);
@@ -75,7 +30,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const int slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6, item = blockIdx.x;
   int64_t nb[P];
   if (P == 1) nb[0] = item;
-  else { nb[0] = (int64_t)(item / a.pair_half) * (2 * a.pair_half) + item % a.pair_half; nb[P - 1] = nb[0] + a.pair_half; }
+  else { nb[0] = pair_first(item, a.pair_half); nb[P - 1] = nb[0] + a.pair_half; }
   const int K = (int)a.K;             // (the host keeps K below 2^27)
   const int r0 = slice * a.rows, r1 = min(K, r0 + a.rows);
 
@@ -250,14 +205,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
 }
 
 template <bool FOUR, int B, int P>
-static void launch(const GemvArgs& a, int items, int W, hipStream_t s) {
+static void launch(const MatArgs& a, int items, int W, hipStream_t s) {
   const dim3 g(items), t(64 * W);
   if (a.norm_w) hipLaunchKernelGGL((gemv_kernel<FOUR, B, P, true>), g, t, 0, s, a);
   else hipLaunchKernelGGL((gemv_kernel<FOUR, B, P, false>), g, t, 0, s, a);
 }
 
 template <bool FOUR, int P>
-static int dispatch_batch(const GemvArgs& a, int batch, int items, int W, hipStream_t s) {
+static int dispatch_batch(const MatArgs& a, int batch, int items, int W, hipStream_t s) {
   switch (batch) {
     case 1: launch<FOUR, 1, P>(a, items, W, s); break;
     case 2: launch<FOUR, 2, P>(a, items, W, s); break;
@@ -284,7 +239,7 @@ static int dispatch_batch(const GemvArgs& a, int batch, int items, int W, hipStr
 struct Plan { int W, rows, P, most, items; };
 static Plan plan(int64_t K, int64_t N, int fmt, int kind, int batch) {
   Plan p;
-  p.P = (kind == FH_EP_SILU_GATE || kind == FH_EP_ROPE_KV) ? 2 : 1;
+  p.P = (kind == FH_EP_SILU_GATE || kind == FH_EP_ROPE_KV) ? 2 : 1;  // as epilogue_args sets MatArgs::P
   p.most = p.P == 1 ? 8 : 4;
   p.items = (int)(N / 16 / p.P);
   const int b = batch < p.most ? batch : p.most;
@@ -314,53 +269,18 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
   if (fmt != FH_BFP8 && fmt != FH_BFP4) return fail(FH_EINVAL, "fh_gemv_bfp: fmt is FH_BFP8 or FH_BFP4");
   if (ldx < K) return fail(FH_EINVAL, "fh_gemv_bfp: ldx < K");
   if (K >= (1LL << 27) || (int64_t)batch * ldx >= (1LL << 31)) return fail(FH_EUNSUP, "fh_gemv_bfp: K or x too large for 32-bit row offsets");
-  GemvArgs a = {};
+  MatArgs a = {};
   a.x = x; a.ldx = ldx;
-  a.mant = (const uint8_t*)w_mant; a.exps = w_exps; a.K = K; a.N = N;
+  a.mant = (const uint8_t*)w_mant; a.exps = w_exps; a.K = K; a.N = N; a.M = batch;
   a.y = y; a.y_bf16 = y_dtype == FH_BF16; a.ldy = ldy;
-  a.kind = ep ? ep->kind : FH_EP_STORE;
-  int64_t out_cols = N;
-  if (ep) {
-    if (ep->norm_w) {
-      if (!ep->ssq_in || K % 16) return fail(FH_EINVAL, "fh_gemv_bfp: RMSNorm prologue needs ssq_in and K a multiple of 16");
-      a.norm_w = ep->norm_w; a.ssq_in = ep->ssq_in; a.ssq_parts = (int)(K / 16); a.eps = ep->eps; a.centered = ep->centered;
-    }
-    switch (ep->kind) {
-      case FH_EP_STORE: a.argmax_parts = (int2*)ep->argmax_parts; break;
-      case FH_EP_RESIDUAL:
-        if (!ep->residual) return fail(FH_EINVAL, "fh_gemv_bfp: FH_EP_RESIDUAL needs residual");
-        a.residual = ep->residual; a.ssq_out = ep->ssq_out;
-        if (y_dtype != FH_F32) return fail(FH_EUNSUP, "fh_gemv_bfp: FH_EP_RESIDUAL writes fp32");
-        break;
-      case FH_EP_SILU_GATE:
-        if (ep->split * 2 != N || ep->split % 16) return fail(FH_EINVAL, "fh_gemv_bfp: FH_EP_SILU_GATE needs N = 2 * split, split a multiple of 16");
-        a.pair_half = ep->split / 16; a.split = ep->split; out_cols = ep->split;
-        break;
-      case FH_EP_ROPE_KV: {
-        const int hd = ep->head_dim;
-        if (hd < 32 || hd % 32 || ep->heads < 1 || ep->kv_heads < 1 || (int64_t)(ep->heads + 2 * ep->kv_heads) * hd != N)
-          return fail(FH_EINVAL, "fh_gemv_bfp: FH_EP_ROPE_KV needs N = (heads + 2 kv_heads) * head_dim, head_dim a multiple of 32");
-        if (!ep->cos_tab || !ep->sin_tab || !ep->places || !ep->cache_rows || !ep->cache || ep->cache_len < 1)
-          return fail(FH_EINVAL, "fh_gemv_bfp: FH_EP_ROPE_KV needs tables, places, cache rows and a cache");
-        if (ep->cache_dtype != FH_F32 && ep->cache_dtype != FH_BF16) return fail(FH_EUNSUP, "fh_gemv_bfp: cache is FH_F32 or FH_BF16");
-        if (y_dtype != FH_F32) return fail(FH_EUNSUP, "fh_gemv_bfp: FH_EP_ROPE_KV writes q in fp32");
-        a.pair_half = hd / 32; out_cols = (int64_t)ep->heads * hd;
-        a.heads = ep->heads; a.kv_heads = ep->kv_heads; a.head_dim = hd;
-        a.cos_tab = ep->cos_tab; a.sin_tab = ep->sin_tab; a.places = ep->places; a.cache_rows = ep->cache_rows;
-        a.cache = ep->cache; a.cache_bf16 = ep->cache_dtype == FH_BF16; a.cache_len = ep->cache_len;
-        break;
-      }
-      default: return fail(FH_EINVAL, "fh_gemv_bfp: unknown epilogue kind");
-    }
-  }
-  if (ldy < out_cols) return fail(FH_EINVAL, "fh_gemv_bfp: ldy smaller than the output's columns");
+  if (int rc = epilogue_args("fh_gemv_bfp", ep, K, N, y_dtype, ldy, a)) return rc;
   const Plan p = plan(K, N, fmt, a.kind, batch);
   a.rows = p.rows;
   hipStream_t s = as_stream(stream);
   const bool four = fmt == FH_BFP4;
   for (int b0 = 0; b0 < batch; b0 += p.most) {  // more rows than a launch takes: several launches, each reading W again
     const int n = batch - b0 < p.most ? batch - b0 : p.most;
-    GemvArgs c = a;
+    MatArgs c = a;
     c.x = (const char*)x + (size_t)b0 * ldx * 4;
     c.y = (char*)y + (size_t)b0 * ldy * (a.y_bf16 ? 2 : 4);
     if (c.ssq_in) c.ssq_in += (int64_t)b0 * c.ssq_parts;

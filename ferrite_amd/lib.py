@@ -34,6 +34,7 @@ SIGNATURES = {
   "fh_bfp_pack": ([P, I, L, L, L, I, I, P, P, P], I),
   "fh_bfp_dequant": ([P, P, L, L, I, I, P, L, P], I),
   "fh_gemv_bfp": ([P, I, L, I, L, L, P, P, I, ctypes.POINTER(Epilogue), P, I, L, P], I),
+  "fh_gemm_bfp": ([P, I, L, L, L, L, P, P, I, ctypes.POINTER(Epilogue), P, I, L, P], I),
   "fh_embed_rows": ([P, I, L, L, P, I, P, P, P], I),
   "fh_attention_workspace_bytes": ([I, I, I, L], S),
   "fh_attention_decode": ([P, P, I, L, I, I, I, I, P, P, L, P, P, S, P], I),

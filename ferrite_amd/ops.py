@@ -71,21 +71,31 @@ def epilogue(kind=lib.EP_STORE, **kw):
   return ep
 
 
-def gemv(x, bw, ep=None, out=None, out_dtype=torch.float32):
-  """y = x @ W with the epilogue ep (fh_gemv_bfp). x [batch][K] fp32; W packed along N."""
+def _matmul(entry, x, bw, ep, out, out_dtype):
   _dev(x)
-  if bw.axis != lib.AXIS_N: raise NotImplementedError("gemv: weights packed along N")
-  if x.dim() != 2 or x.shape[1] != bw.K or x.stride(1) != 1: raise ValueError(f"gemv: x {tuple(x.shape)} for W {bw.K}x{bw.N}")
-  batch = x.shape[0]
+  if bw.axis != lib.AXIS_N: raise NotImplementedError(f"{entry}: weights packed along N")
+  if x.dim() != 2 or x.shape[1] != bw.K or x.stride(1) != 1: raise ValueError(f"{entry}: x {tuple(x.shape)} for W {bw.K}x{bw.N}")
+  rows = x.shape[0]
   if out is None:
     cols = bw.N
     if ep is not None and ep.kind == lib.EP_SILU_GATE: cols = ep.split
     if ep is not None and ep.kind == lib.EP_ROPE_KV: cols = ep.heads * ep.head_dim
-    out = torch.empty(batch, cols, dtype=out_dtype, device=x.device)
-  lib.call("fh_gemv_bfp", _ptr(x), _TORCH[x.dtype], x.stride(0), batch, bw.K, bw.N, _ptr(bw.mant), _ptr(bw.exps),
+    out = torch.empty(rows, cols, dtype=out_dtype, device=x.device)
+  _dev(out)
+  lib.call(entry, _ptr(x), _TORCH[x.dtype], x.stride(0), rows, bw.K, bw.N, _ptr(bw.mant), _ptr(bw.exps),
            lib.DTYPES[bw.fmt], ctypes.byref(ep) if ep is not None else None, _ptr(out), _TORCH[out.dtype], out.stride(0),
            _stream())
   return out
+
+
+def gemv(x, bw, ep=None, out=None, out_dtype=torch.float32):
+  """y = x @ W with the epilogue ep (fh_gemv_bfp): a few rows, fp32 x, exact products. W packed along N."""
+  return _matmul("fh_gemv_bfp", x, bw, ep, out, out_dtype)
+
+
+def gemm(x, bw, ep=None, out=None, out_dtype=torch.float32):
+  """y = x @ W with the epilogue ep (fh_gemm_bfp): many rows on the matrix cores, x (fp32 or bf16) rounded to bf16."""
+  return _matmul("fh_gemm_bfp", x, bw, ep, out, out_dtype)
 
 
 def embed_rows(table, ids, x=None, ssq=None):

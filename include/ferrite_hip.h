@@ -69,8 +69,9 @@ int fh_bfp_pack(const void* src, int src_dtype, int64_t K, int64_t N, int64_t ld
 int fh_bfp_dequant(const void* mant, const uint8_t* exps, int64_t K, int64_t N, int fmt, int axis, uint16_t* out,
                    int64_t ldo, void* stream);
 
-/* ---- decode GEMV: y = x @ W with W a block float, batch 1..16, fused prologue and epilogue ----------------------
- * x: [batch][K] fp32 (row stride ldx). Products are exact and sums are fp32.
+/* ---- decode GEMV: y = x @ W with W a block float, a few rows, fused prologue and epilogue -------------------------
+ * x: [batch][K] fp32 (row stride ldx). Products are exact and sums are fp32. Up to 8 rows (4 with a paired epilogue)
+ * share one pass over W; more rows take more passes (fh_gemm_bfp is the kernel for many rows).
  * Replaces the bfp-B matmul of fused_kernel (ferrite/compiler.py:699-1111, matmul at 958-1022) for a token row
  * (compiler.py:838-845), with the elementwise ops models/llama.py puts after it fused into the same kernel. */
 
@@ -113,6 +114,16 @@ typedef struct fh_epilogue {
 int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, int64_t K, int64_t N, const void* w_mant,
                 const uint8_t* w_exps, int fmt, const fh_epilogue* ep, void* y, int y_dtype, int64_t ldy, void* stream);
 
+/* ---- prefill GEMM: the same y = epilogue(prologue(x) @ W) for M rows, on the matrix cores ----------------------
+ * x: [M][K] fp32 or bf16 (row stride ldx, a multiple of 8); K a multiple of 32. As ferrite's chip does (its unpacker
+ * hands the matrix unit bf16; ferrite/tensor.py:443-485), the products are bf16 x bf16 with fp32 sums: x (times the
+ * RMSNorm weight) is rounded to bf16 (nearest even), the weight's values are exact. Every epilogue of fh_gemv_bfp,
+ * with [M] in place of [batch] (FH_EP_ROPE_KV: each row its own place and cache row, a prompt's tokens at once).
+ * Replaces fused_kernel's matmul for prompt rows (ferrite/compiler.py:699-1111 over 32-row tiles; models/llama.py's
+ * prefill, 498-504). No scratch memory; results do not depend on timing. */
+int fh_gemm_bfp(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int64_t N, const void* w_mant,
+                const uint8_t* w_exps, int fmt, const fh_epilogue* ep, void* y, int y_dtype, int64_t ldy, void* stream);
+
 /* ---- the rest of a decode step ------------------------------------------------------------------------------- */
 
 /* Rows ids[batch] of an embedding table [vocab][dim] (fp32 or bf16) into x[batch][dim] fp32, with the sums of
@@ -124,8 +135,9 @@ int fh_embed_rows(const void* table, int table_dtype, int64_t vocab, int64_t dim
 /* Decode attention over a KV cache (models/llama.py:129-142; Tensor.attend, ferrite/tensor.py:487-516): for each
  * row b and query head h, softmax(q k^T / sqrt(head_dim)) v over the cache rows first_row[b] .. first_row[b] +
  * places[b] (those its place reaches), k and v the heads of kv head h / (heads / kv_heads) (grouped-query).
- * q, o: [batch][heads*head_dim] fp32. Flash decoding: the keys are shared out among workgroups in chunks and the
- * chunks' results combined by exp-weights in the last workgroup to finish (ferrite/compiler.py:1138-1145). */
+ * q, o: [batch][heads*head_dim] fp32. Flash decoding: the keys are shared out among workgroups in chunks of 128
+ * rows, each writing its partial result and softmax statistics to the workspace, and a second kernel combines the
+ * chunks by exp-weights (ferrite/compiler.py:1138-1145); a context of one chunk writes o directly. */
 size_t fh_attention_workspace_bytes(int batch, int heads, int head_dim, int64_t max_context);
 int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch, int heads,
                         int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row, int64_t max_context,
