@@ -53,6 +53,21 @@ __device__ inline void magnitudes(const uint2& m, float (&f)[16]) {
   }
 }
 
+// 8 of a run's 16 magnitudes (columns 8h .. 8h + 7 of a row): bfp8's 8 bytes, bfp4's 4 bytes (16 q as above)
+__device__ inline void magnitudes8(const uint2& m, float (&f)[8]) {
+  const uint32_t w[2] = {m.x, m.y};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = (float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 255u);
+}
+__device__ inline void magnitudes8(const uint32_t& m, float (&f)[8]) {
+  const uint32_t hi = m & 0xF0F0F0F0u, lo = (m << 4) & 0xF0F0F0F0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = (float)(int8_t)((lo >> (8 * i)) & 255u);
+    f[2 * i + 1] = (float)(int8_t)((hi >> (8 * i)) & 255u);
+  }
+}
+
 // A pair item's first run: pairs are (nb0, nb0 + half) within each group of 2 half runs (a head's two halves for
 // RoPE, where half = head_dim / 32; gate and up for SiLU·gate, where half = split / 16 and there is one group).
 __host__ __device__ inline int64_t pair_first(int64_t item, int half) { return item / half * (2 * half) + item % half; }

@@ -4,11 +4,12 @@
 // As on ferrite's chip (the unpacker feeds bf16 to the matrix unit; ferrite/tensor.py:443-485), the products are bf16 x
 // bf16 with fp32 sums: x (times the RMSNorm weight) is rounded to bf16, and the weight's values q * 2^(e - 133) are
 // exact in bf16 (at most 7 significant bits). A workgroup of 4 waves computes a 128 x 128 tile (8 runs of 16 columns,
-// or 4 runs and their RoPE / SiLU·gate partners) in K steps of 64: its threads load the next step's x rows and weight
-// rows from HBM into registers while the matrix cores work on the current step from LDS, then convert: x to bf16 rows,
-// the weight's 16-byte runs to bf16 columns (K-contiguous, as v_mfma_f32_16x16x32_bf16 takes its operands). Each wave
-// owns a 64 x 64 quarter: 4 x 4 blocks of 16 x 16, 32 MFMAs a step. The epilogue stages the tile in LDS as fp32 so
-// that each output sees its row's 1/rms and its pair partner, whichever wave computed it.
+// or 4 runs and their RoPE / SiLU·gate partners) in K steps of 64, the operands in two LDS stages: while the matrix
+// cores work on one stage, the threads' loads of the next step's x rows and weight rows are in flight, and once the
+// step's products are issued they convert them into the other stage: x to bf16 rows, the weight's 16-byte runs to bf16
+// columns (K-contiguous, as v_mfma_f32_32x32x16_bf16 takes its operands). One barrier a step. Each wave owns a 64 x 64
+// quarter, 2 x 2 blocks of 32 x 32, 16 MFMAs a step. The epilogue stages the tile in LDS as fp32 so that each output
+// sees its row's 1/rms and its pair partner, whichever wave computed it.
 //
 // Tiles go to the XCDs in contiguous ranges (the hardware deals workgroups round-robin over the 8 XCDs) and within a
 // range in groups of 8 row tiles, so that an XCD's L2 keeps both the weight columns and the x rows it re-reads.
@@ -21,10 +22,11 @@ constexpr int GM_LD = GM_BK + 8;     // LDS row of a tile operand, bf16: 144 byt
 constexpr int GM_LDC = GM_BN + 4;    // LDS row of the fp32 output tile
 constexpr int GM_THREADS = 256;
 constexpr int GM_GROUP = 8;          // row tiles a group (tile order)
-constexpr int GM_LDS = GM_BM * GM_LDC * 4;  // 67,584 bytes: the output tile; the operand tiles (2 x 18,432) alias it
+constexpr int GM_STAGE = 2 * GM_BM * GM_LD * 2;  // one stage: x [128][72] and W [128][72], bf16: 36,864 bytes
+constexpr int GM_LDS = 2 * GM_STAGE;         // 73,728 bytes; the fp32 output tile [128][132] (67,584) aliases them
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
 
 __device__ inline uint32_t pack_bf16_exact(float lo, float hi) {  // both exact in bf16: the high halves
   return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
@@ -43,12 +45,11 @@ __device__ inline int64_t tile_run(const MatArgs& a, int tn, int lr) {
   return lr < 4 ? nb0 : nb0 + a.pair_half;
 }
 
-template <bool FOUR, bool XBF16>
+template <bool FOUR, bool XBF16, bool NORM>
 __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(16))) char smem[GM_LDS];
   __shared__ float rs_s[GM_BM];
-  uint16_t* As = (uint16_t*)smem;                      // [128 rows][72]: x, bf16
-  uint16_t* Bs = (uint16_t*)(smem + GM_BM * GM_LD * 2); // [128 columns][72]: W, bf16, K-contiguous
+  // stage s: x at smem + s * GM_STAGE ([128 rows][72] bf16), W after it ([128 columns][72] bf16, K-contiguous)
   float* Cs = (float*)smem;                            // [128][132]: the output tile (after the K loop)
 
   // tile order
@@ -64,63 +65,66 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int K = (int)a.K;
 
-  // this thread's loads: x row ar (of 128), k half ah (32 values); weight run lr (of 8), rows 2 rp and 2 rp + 1
+  // this thread's loads: x row ar (of 128), k half ah (32 values); weight run lr (of 8), rows 4 rq .. 4 rq + 3,
+  // columns 8 ch .. 8 ch + 7
   const int ar = t >> 1, ah = t & 1;
   const int64_t xrow = min(m0 + ar, a.M - 1);
   const bool xok = m0 + ar < a.M;
-  const int lr = t >> 5, rp = t & 31;
+  const int lr = t >> 5, rq = (t & 31) >> 1, ch = t & 1;
   const int64_t nb = tile_run(a, tn, lr);
   constexpr int RB = FOUR ? 8 : 16;
-  const uint8_t* mrun = a.mant + (nb < 0 ? 0 : nb) * a.K * RB;
+  const uint8_t* mrun = a.mant + (nb < 0 ? 0 : nb) * a.K * RB + ch * (RB / 2);
   const uint8_t* erun = a.exps + (nb < 0 ? 0 : nb) * a.K;
 
-  using Row = typename std::conditional<FOUR, uint2, uint4>::type;
-  float4 xf[8];      // fp32 x: 32 values
-  uint4 xb[4];       // bf16 x: 32 values
-  Row wm[2];
-  uint32_t we;
+  // a K step's loads, in registers: two sets, so that each step's loads have two steps' compute to arrive
+  using Half = typename std::conditional<FOUR, uint32_t, uint2>::type;  // 8 of a row's 16 magnitudes
+  constexpr int XW = XBF16 ? 4 : 8;  // x's 32 values: 4 x 16 bytes (bf16) or 8 (fp32), as uint4
 
-  auto load = [&](int k0) {
-    const int kx = k0 + 32 * ah;
-    if (XBF16) {
-      const uint16_t* p = (const uint16_t*)a.x + xrow * a.ldx;
+  // Loads are unconditional (addresses clamped into the tensors) so that the compiler can count them and wait only
+  // for the older set: x's k past K reads the row's last 32 values, whose weight rows are zero; a step past the last
+  // re-reads the last.
+  const int last = (K - 1) / GM_BK * GM_BK;
+  auto load = [&](int k0, uint4 (&xr)[XW], Half (&wm)[4], uint32_t& we) {
+    k0 = min(k0, last);
+    const int kx = min(k0 + 32 * ah, K - 32);
+    const uint4* p = (const uint4*)((const char*)a.x + (xrow * a.ldx + kx) * (XBF16 ? 2 : 4));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xb[i] = kx + 8 * i < K ? *(const uint4*)(p + kx + 8 * i) : make_uint4(0, 0, 0, 0);
-    } else {
-      const float* p = (const float*)a.x + xrow * a.ldx;
+    for (int i = 0; i < XW; ++i) xr[i] = p[i];
+    const int k = min(k0 + 4 * rq, K - 4);  // (K is a multiple of 32)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xf[i] = kx + 4 * i < K ? *(const float4*)(p + kx + 4 * i) : make_float4(0, 0, 0, 0);
-    }
-    const int k = min(k0 + 2 * rp, K - 2);  // (K is even; rows past K meet zero x)
-    wm[0] = *(const Row*)(mrun + (int64_t)k * RB);
-    wm[1] = *(const Row*)(mrun + (int64_t)(k + 1) * RB);
-    we = *(const uint16_t*)(erun + k);
+    for (int r = 0; r < 4; ++r) wm[r] = *(const Half*)(mrun + (int64_t)(k + r) * RB);
+    we = *(const uint32_t*)(erun + k);
   };
 
-  auto store = [&](int k0) {
+  auto store = [&](int k0, int stage, const uint4 (&xr)[XW], const Half (&wm)[4], uint32_t we) {
+    uint16_t* As = (uint16_t*)(smem + stage * GM_STAGE);
+    uint16_t* Bs = As + GM_BM * GM_LD;
     // x -> bf16 (times the RMSNorm weight), 4 x 16 bytes
-    const int kx = k0 + 32 * ah;
-    uint4 out[4];
-    if (XBF16 && !a.norm_w) {
+    const int kx = min(k0 + 32 * ah, K - 32);
+    if (XBF16 && !NORM) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) out[i] = xb[i];
+      for (int i = 0; i < 4; ++i)  // (element by element: a whole-array copy became a memcpy through scratch)
+        *(uint4*)(As + ar * GM_LD + 32 * ah + 8 * i) = make_uint4(xr[i].x, xr[i].y, xr[i].z, xr[i].w);
     } else {
       float v[32];
       if (XBF16) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint32_t w4[4] = {xb[i].x, xb[i].y, xb[i].z, xb[i].w};
+          const uint32_t w4[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
 #pragma unroll
           for (int j = 0; j < 4; ++j) { v[8 * i + 2 * j] = __uint_as_float(w4[j] << 16); v[8 * i + 2 * j + 1] = __uint_as_float(w4[j] & 0xFFFF0000u); }
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { v[4 * i] = xf[i].x; v[4 * i + 1] = xf[i].y; v[4 * i + 2] = xf[i].z; v[4 * i + 3] = xf[i].w; }
+        for (int i = 0; i < 8; ++i) {
+          v[4 * i] = __uint_as_float(xr[i].x); v[4 * i + 1] = __uint_as_float(xr[i].y);
+          v[4 * i + 2] = __uint_as_float(xr[i].z); v[4 * i + 3] = __uint_as_float(xr[i].w);
+        }
       }
-      if (a.norm_w) {
+      if (NORM) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          float4 g = kx + 4 * i < K ? *(const float4*)(a.norm_w + kx + 4 * i) : make_float4(0, 0, 0, 0);
+          float4 g = *(const float4*)(a.norm_w + kx + 4 * i);
           if (a.centered) { g.x += 1.f; g.y += 1.f; g.z += 1.f; g.w += 1.f; }
           v[4 * i] *= g.x; v[4 * i + 1] *= g.y; v[4 * i + 2] *= g.z; v[4 * i + 3] *= g.w;
         }
@@ -131,28 +135,33 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        out[i] = make_uint4(pack_bf16_rne(v[8 * i], v[8 * i + 1]), pack_bf16_rne(v[8 * i + 2], v[8 * i + 3]),
-                            pack_bf16_rne(v[8 * i + 4], v[8 * i + 5]), pack_bf16_rne(v[8 * i + 6], v[8 * i + 7]));
+        *(uint4*)(As + ar * GM_LD + 32 * ah + 8 * i) =
+            make_uint4(pack_bf16_rne(v[8 * i], v[8 * i + 1]), pack_bf16_rne(v[8 * i + 2], v[8 * i + 3]),
+                       pack_bf16_rne(v[8 * i + 4], v[8 * i + 5]), pack_bf16_rne(v[8 * i + 6], v[8 * i + 7]));
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *(uint4*)(As + ar * GM_LD + 32 * ah + 8 * i) = out[i];
 
-    // the weight's two rows -> 16 columns of 2 bf16 each; rows past K (clamped loads) are zero here too
-    float f0[16], f1[16];
-    magnitudes(wm[0], f0);
-    magnitudes(wm[1], f1);
-    const bool r0ok = k0 + 2 * rp < K;
-    const float s0 = r0ok ? ldexpf(1.f, (int)(we & 255u) - 133) : 0.f;
-    const float s1 = r0ok ? ldexpf(1.f, (int)(we >> 8) - 133) : 0.f;
+    // the weight's 4 rows x 8 columns -> 8 columns of 4 bf16 (one 8-byte LDS write each); rows past K are zero
+    float f[4][8];
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
-      *(uint32_t*)(Bs + (lr * 16 + c) * GM_LD + 2 * rp) = pack_bf16_exact(f0[c] * s0, f1[c] * s1);
+    for (int r = 0; r < 4; ++r) magnitudes8(wm[r], f[r]);
+    const bool ok = k0 + 4 * rq < K;
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = ok ? ldexpf(1.f, (int)((we >> (8 * r)) & 255u) - 133) : 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      *(uint2*)(Bs + (lr * 16 + ch * 8 + c) * GM_LD + 4 * rq) =
+          make_uint2(pack_bf16_exact(f[0][c] * sc[0], f[1][c] * sc[1]), pack_bf16_exact(f[2][c] * sc[2], f[3][c] * sc[3]));
   };
 
-  load(0);
+  uint4 x0[XW], x1[XW];
+  Half w0[4], w1[4];
+  uint32_t e0, e1;
+  load(0, x0, w0, e0);
+  load(GM_BK, x1, w1, e1);
 
   // each row's 1 / rms from the sums of squares its maker left by runs of 16 (two threads a row)
-  if (a.norm_w) {
+  if (NORM) {
     float s = 0.f;
     if (xok) {
       const float* q = a.ssq_in + xrow * a.ssq_parts;
@@ -164,41 +173,56 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
     rs_s[ar] = 1.f;
   }
 
-  floatx4 acc[4][4];
+  floatx16 acc[2][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
-  const int fr = lane & 15, fk = 8 * (lane >> 4);
-  for (int k0 = 0; k0 < K; k0 += GM_BK) {
-    __syncthreads();            // the previous step's operands are read
-    store(k0);
-    __syncthreads();
-    if (k0 + GM_BK < K) load(k0 + GM_BK);
+  const int fr = lane & 31, fk = 8 * (lane >> 5);
+  auto compute = [&](int stage) {
+    const uint16_t* As = (const uint16_t*)(smem + stage * GM_STAGE);
+    const uint16_t* Bs = As + GM_BM * GM_LD;
 #pragma unroll
-    for (int kk = 0; kk < GM_BK; kk += 32) {
-      bf16x8 af[4], bfr[4];
+    for (int kk = 0; kk < GM_BK; kk += 16) {
+      bf16x8 af[2], bfr[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = *(const bf16x8*)(As + (wr + 16 * i + fr) * GM_LD + kk + fk);
+      for (int i = 0; i < 2; ++i) af[i] = *(const bf16x8*)(As + (wr + 32 * i + fr) * GM_LD + kk + fk);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bfr[j] = *(const bf16x8*)(Bs + (wc + 16 * j + fr) * GM_LD + kk + fk);
+      for (int j = 0; j < 2; ++j) bfr[j] = *(const bf16x8*)(Bs + (wc + 32 * j + fr) * GM_LD + kk + fk);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
+  };
+  // step i computes stage i % 2 from the LDS, issues step i + 2's loads into the registers step i's came in, and
+  // stores step i + 1's (loaded during step i - 1) into the other stage
+  store(0, 0, x0, w0, e0);
+  for (int k0 = 0; k0 < K; k0 += 2 * GM_BK) {  // (an odd count of steps ends with a step of zero weights)
+    __syncthreads();            // stage 0 is stored; stage 1's readers are done
+    load(k0 + 2 * GM_BK, x0, w0, e0);
+    compute(0);
+    store(k0 + GM_BK, 1, x1, w1, e1);
+    __syncthreads();
+    load(k0 + 3 * GM_BK, x1, w1, e1);
+    compute(1);
+    store(k0 + 2 * GM_BK, 0, x0, w0, e0);  // (past the last step: a stage nobody reads)
   }
 
-  // the output tile, fp32, through LDS: block (i, j)'s value r of lane l is row 4 (l / 16) + r, column l % 16
+  // the output tile, fp32, through LDS: block (i, j)'s value r of lane l is row 8 (r / 4) + 4 (l / 32) + r % 4,
+  // column l % 32
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Cs[(wr + 16 * i + 4 * (lane >> 4) + r) * GM_LDC + wc + 16 * j + (lane & 15)] = acc[i][j][r];
+      for (int r = 0; r < 16; ++r)
+        Cs[(wr + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * GM_LDC + wc + 32 * j + (lane & 31)] = acc[i][j][r];
   __syncthreads();
 
   const int kind = a.kind;
@@ -288,13 +312,17 @@ extern "C" int fh_gemm_bfp(const void* x, int x_dtype, int64_t ldx, int64_t M, i
   if (tiles_m * tiles_n >= (1LL << 31)) return fail(FH_EUNSUP, "fh_gemm_bfp: too many tiles");
   const dim3 g((unsigned)(tiles_m * tiles_n)), b(GM_THREADS);
   hipStream_t s = as_stream(stream);
-  const bool four = fmt == FH_BFP4;
-  if (four) {
-    if (a.x_bf16) hipLaunchKernelGGL((gemm_kernel<true, true>), g, b, 0, s, a, (int)tiles_m, (int)tiles_n);
-    else hipLaunchKernelGGL((gemm_kernel<true, false>), g, b, 0, s, a, (int)tiles_m, (int)tiles_n);
-  } else {
-    if (a.x_bf16) hipLaunchKernelGGL((gemm_kernel<false, true>), g, b, 0, s, a, (int)tiles_m, (int)tiles_n);
-    else hipLaunchKernelGGL((gemm_kernel<false, false>), g, b, 0, s, a, (int)tiles_m, (int)tiles_n);
+  const int tm = (int)tiles_m, tn = (int)tiles_n;
+  const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
+  switch (which) {
+    case 0: hipLaunchKernelGGL((gemm_kernel<false, false, false>), g, b, 0, s, a, tm, tn); break;
+    case 1: hipLaunchKernelGGL((gemm_kernel<false, false, true>), g, b, 0, s, a, tm, tn); break;
+    case 2: hipLaunchKernelGGL((gemm_kernel<false, true, false>), g, b, 0, s, a, tm, tn); break;
+    case 3: hipLaunchKernelGGL((gemm_kernel<false, true, true>), g, b, 0, s, a, tm, tn); break;
+    case 4: hipLaunchKernelGGL((gemm_kernel<true, false, false>), g, b, 0, s, a, tm, tn); break;
+    case 5: hipLaunchKernelGGL((gemm_kernel<true, false, true>), g, b, 0, s, a, tm, tn); break;
+    case 6: hipLaunchKernelGGL((gemm_kernel<true, true, false>), g, b, 0, s, a, tm, tn); break;
+    default: hipLaunchKernelGGL((gemm_kernel<true, true, true>), g, b, 0, s, a, tm, tn); break;
   }
   return check_launch("fh_gemm_bfp");
 }
