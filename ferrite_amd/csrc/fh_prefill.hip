@@ -1,0 +1,261 @@
+// A prompt's causal attention on the matrix cores, and the row RMSNorm that hands the prefill GEMMs bf16 rows.
+//
+// Attention (models/llama.py:129-142 for a chunk of T consecutive places p0 .. p0 + T - 1 of one sequence, whose
+// keys and values are already in the cache: its own rows and every earlier place of the slot). A workgroup of 4 waves
+// takes 128 query rows of one query head, a wave 32 of them, and walks the keys in tiles of 64 that its rows reach.
+// The scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_bf16, keys down, queries across), so that a lane
+// holds one query's scores: its softmax statistics need no cross-lane work beyond the two halves of the wave. The
+// online softmax (a running max and sum, rescaling the partial output) follows flash attention; the output is
+// accumulated transposed too, O^T += V^T P^T, with P^T taken straight from the score registers: the order of the keys
+// inside a 16-key step does not change the sum, so V^T is read from LDS in the order the score layout holds them.
+// q, k, v go to bf16 for the matrix cores (as ferrite's chip holds them); scores, softmax and sums are fp32. Masked
+// scores are -1e30 (the reference adds -1e9; either leaves exp() at 0). Query tiles are issued longest first.
+#include <math.h>
+#include "fh_common.h"
+
+namespace fh {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
+
+constexpr int PA_BQ = 128;      // query rows a workgroup (32 a wave)
+constexpr int PA_BK = 64;       // keys a tile
+constexpr float PA_MASKED = -1e30f;
+
+struct PrefArgs {
+  const float* q; int64_t ldq;
+  const void* cache; int64_t cache_len;
+  int T, heads, kv_heads; float scale;
+  int64_t p0, slot_row;
+  void* o; int64_t ldo; int o_bf16;
+};
+
+__device__ inline uint32_t pack2_rne(float lo, float hi) { return bf16_rne_f(lo) | (bf16_rne_f(hi) << 16); }
+
+template <int HD, bool CBF16>
+__global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
+  constexpr int KLD = HD + 8;        // K tile row in LDS (bf16): 16-byte aligned, banks spread
+  constexpr int VLD = PA_BK + 8;     // V^T tile row (bf16)
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[PA_BK * KLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[HD * VLD];
+
+  const int ntiles = (a.T + PA_BQ - 1) / PA_BQ;
+  const int qt = ntiles - 1 - (int)blockIdx.x, h = blockIdx.y;  // the longest tiles first
+  const int kvh = h / (a.heads / a.kv_heads);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int ql = lane & 31, hh = lane >> 5;
+  const int qrow = qt * PA_BQ + wave * 32 + ql;            // this lane's query row
+  const int qr = min(qrow, a.T - 1);
+  const int64_t qplace = a.p0 + qr;
+  const int64_t last_key = a.p0 + min(qt * PA_BQ + PA_BQ, a.T) - 1;  // the workgroup's last key (its last row's place)
+  const int nkt = (int)(last_key / PA_BK) + 1;
+
+  // the lane's query, bf16, in the B-operand layout: step s holds dimensions 16 s + 8 hh .. + 7
+  bf16x8 qf[HD / 16];
+  {
+    const float* qp = a.q + (int64_t)qr * a.ldq + (int64_t)h * HD;
+#pragma unroll
+    for (int s = 0; s < HD / 16; ++s) {
+      const float4 u = *(const float4*)(qp + 16 * s + 8 * hh), v = *(const float4*)(qp + 16 * s + 8 * hh + 4);
+      const float f[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[s][i] = (__bf16)f[i];
+    }
+  }
+
+  floatx16 acc[HD / 32];
+#pragma unroll
+  for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[d][r] = 0.f;
+  float m = PA_MASKED, l = 0.f;
+
+  const size_t esz = CBF16 ? 2 : 4;
+  const char* kbase = (const char*)a.cache + ((int64_t)kvh * a.cache_len + a.slot_row) * HD * esz;
+  const char* vbase = (const char*)a.cache + ((int64_t)(a.kv_heads + kvh) * a.cache_len + a.slot_row) * HD * esz;
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int64_t k0 = (int64_t)kt * PA_BK;
+    __syncthreads();  // the previous tile's readers are done
+    // K tile: 64 rows x HD, a thread 16 bytes of bf16 at a time
+    for (int i = t; i < PA_BK * HD / 8; i += 256) {
+      const int r = i / (HD / 8), c = (i % (HD / 8)) * 8;
+      const int64_t key = min(k0 + r, last_key);
+      uint4 w;
+      if (CBF16) {
+        w = *(const uint4*)(kbase + (key * HD + c) * 2);
+      } else {
+        const float4 u = *(const float4*)(kbase + (key * HD + c) * 4), v = *(const float4*)(kbase + (key * HD + c + 4) * 4);
+        w = make_uint4(pack2_rne(u.x, u.y), pack2_rne(u.z, u.w), pack2_rne(v.x, v.y), pack2_rne(v.z, v.w));
+      }
+      *(uint4*)(Ks + r * KLD + c) = w;
+    }
+    // V^T tile: a thread 4 keys x 8 dimensions, written as 8 rows of 4 keys
+    for (int i = t; i < (PA_BK / 4) * (HD / 8); i += 256) {
+      const int kq = i % (PA_BK / 4), dg = i / (PA_BK / 4);
+      uint32_t lo[4][4];  // [key][pair of dims]
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t key = min(k0 + 4 * kq + j, last_key);
+        if (CBF16) {
+          const uint4 w = *(const uint4*)(vbase + (key * HD + 8 * dg) * 2);
+          lo[j][0] = w.x; lo[j][1] = w.y; lo[j][2] = w.z; lo[j][3] = w.w;
+        } else {
+          const float4 u = *(const float4*)(vbase + (key * HD + 8 * dg) * 4), v = *(const float4*)(vbase + (key * HD + 8 * dg + 4) * 4);
+          lo[j][0] = pack2_rne(u.x, u.y); lo[j][1] = pack2_rne(u.z, u.w); lo[j][2] = pack2_rne(v.x, v.y); lo[j][3] = pack2_rne(v.z, v.w);
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const int sh = 16 * (d & 1), p = d >> 1;
+        const uint32_t k01 = ((lo[0][p] >> sh) & 0xFFFFu) | (((lo[1][p] >> sh) & 0xFFFFu) << 16);
+        const uint32_t k23 = ((lo[2][p] >> sh) & 0xFFFFu) | (((lo[3][p] >> sh) & 0xFFFFu) << 16);
+        *(uint2*)(Vt + (8 * dg + d) * VLD + 4 * kq) = make_uint2(k01, k23);
+      }
+    }
+    __syncthreads();
+
+    // S^T for the tile's two blocks of 32 keys: block kb's value r of lane (ql, hh) is key 32 kb + 8 (r / 4) + 4 hh +
+    // r % 4, query ql
+    floatx16 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+#pragma unroll
+      for (int st = 0; st < HD / 16; ++st) {
+        const bf16x8 kf = *(const bf16x8*)(Ks + (32 * kb + ql) * KLD + 16 * st + 8 * hh);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kb], 0, 0, 0);
+      }
+    }
+    // scale, mask past the query's place, and the online softmax
+    float mt = PA_MASKED;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hh + (r & 3);
+        const float v = key <= qplace ? s[kb][r] * a.scale : PA_MASKED;
+        s[kb][r] = v;
+        mt = fmaxf(mt, v);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m, mt);
+    const float alpha = __expf(m - mn);
+    float rsum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __expf(s[kb][r] - mn);
+        s[kb][r] = p;
+        rsum += p;
+      }
+    rsum += __shfl_xor(rsum, 32, 64);
+    l = l * alpha + rsum;
+    m = mn;
+#pragma unroll
+    for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[d][r] *= alpha;
+    // O^T += V^T P^T, 16 keys a step: the keys of score registers 8 j .. 8 j + 7 of block kb, which are
+    // 32 kb + 16 j + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        bf16x8 pf;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pf[i] = (__bf16)s[kb][8 * j + i];
+        const int g = 32 * kb + 16 * j;
+#pragma unroll
+        for (int d = 0; d < HD / 32; ++d) {
+          const uint16_t* row = Vt + (32 * d + ql) * VLD + g;
+          const uint2 v0 = *(const uint2*)(row + 4 * hh), v1 = *(const uint2*)(row + 8 + 4 * hh);
+          const uint4 vv = make_uint4(v0.x, v0.y, v1.x, v1.y);
+          acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)&vv, pf, acc[d], 0, 0, 0);
+        }
+      }
+  }
+
+  // o[row][h * HD + dim]: block d's value r of lane (ql, hh) is dimension 32 d + 8 (r / 4) + 4 hh + r % 4
+  if (qrow < a.T) {
+    const float inv = 1.f / l;
+    const int64_t base = (int64_t)qrow * a.ldo + (int64_t)h * HD;
+#pragma unroll
+    for (int d = 0; d < HD / 32; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dim = 32 * d + 8 * g + 4 * hh;
+        const float v0 = acc[d][4 * g] * inv, v1 = acc[d][4 * g + 1] * inv, v2 = acc[d][4 * g + 2] * inv, v3 = acc[d][4 * g + 3] * inv;
+        if (a.o_bf16) *(uint2*)((uint16_t*)a.o + base + dim) = make_uint2(pack2_rne(v0, v1), pack2_rne(v2, v3));
+        else *(float4*)((float*)a.o + base + dim) = make_float4(v0, v1, v2, v3);
+      }
+  }
+}
+
+// out = x * rsqrt(mean(x^2) + eps) * w (w + 1 when centered), a workgroup a row (models/llama.py:82-85)
+template <bool OBF16>
+__global__ __launch_bounds__(256) void rms_rows_kernel(const float* x, int64_t ldx, int dim, const float* w, float eps,
+                                                       int centered, void* out, int64_t ldo) {
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * ldx;
+  float s = 0.f;
+  for (int i = threadIdx.x; i < dim; i += 256) s += xr[i] * xr[i];
+  s = wave_sum(s);
+  __shared__ float part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  const float rs = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)dim + eps);
+  for (int i = threadIdx.x; i < dim; i += 256) {
+    const float g = centered ? w[i] + 1.f : w[i];
+    const float v = xr[i] * rs * g;
+    if (OBF16) ((uint16_t*)out)[row * ldo + i] = (uint16_t)bf16_rne_f(v);
+    else ((float*)out)[row * ldo + i] = v;
+  }
+}
+
+}  // namespace fh
+
+using namespace fh;
+
+extern "C" int fh_attention_prefill(const float* q, int64_t ldq, const void* cache, int cache_dtype, int64_t cache_len,
+                                    int T, int heads, int kv_heads, int head_dim, int64_t p0, int64_t slot_row, void* o,
+                                    int o_dtype, int64_t ldo, void* stream) {
+  if (!q || !cache || !o) return fail(FH_EINVAL, "fh_attention_prefill: null pointer");
+  if (T < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads) return fail(FH_EINVAL, "fh_attention_prefill: need T >= 1, heads a multiple of kv_heads");
+  if (head_dim != 64 && head_dim != 128) return fail(FH_EUNSUP, "fh_attention_prefill: head_dim 64 or 128");
+  if (cache_dtype != FH_F32 && cache_dtype != FH_BF16) return fail(FH_EUNSUP, "fh_attention_prefill: cache is FH_F32 or FH_BF16");
+  if (o_dtype != FH_F32 && o_dtype != FH_BF16) return fail(FH_EINVAL, "fh_attention_prefill: o is FH_F32 or FH_BF16");
+  if (ldq < (int64_t)heads * head_dim || ldo < (int64_t)heads * head_dim || ldq % 4 || ldo % 4)
+    return fail(FH_EINVAL, "fh_attention_prefill: ldq and ldo at least heads * head_dim, multiples of 4");
+  if (p0 < 0 || slot_row < 0 || slot_row + p0 + T > cache_len)
+    return fail(FH_EINVAL, "fh_attention_prefill: the rows' keys (slot_row .. slot_row + p0 + T - 1) must lie in the cache");
+  PrefArgs a = {};
+  a.q = q; a.ldq = ldq; a.cache = cache; a.cache_len = cache_len;
+  a.T = T; a.heads = heads; a.kv_heads = kv_heads; a.scale = 1.0f / sqrtf((float)head_dim);
+  a.p0 = p0; a.slot_row = slot_row; a.o = o; a.ldo = ldo; a.o_bf16 = o_dtype == FH_BF16;
+  const dim3 g((T + PA_BQ - 1) / PA_BQ, heads), b(256);
+  hipStream_t s = as_stream(stream);
+  const bool bf = cache_dtype == FH_BF16;
+  if (head_dim == 128) {
+    if (bf) hipLaunchKernelGGL((attention_prefill_kernel<128, true>), g, b, 0, s, a);
+    else hipLaunchKernelGGL((attention_prefill_kernel<128, false>), g, b, 0, s, a);
+  } else {
+    if (bf) hipLaunchKernelGGL((attention_prefill_kernel<64, true>), g, b, 0, s, a);
+    else hipLaunchKernelGGL((attention_prefill_kernel<64, false>), g, b, 0, s, a);
+  }
+  return check_launch("fh_attention_prefill");
+}
+
+extern "C" int fh_rms_rows(const float* x, int64_t ldx, int64_t rows, int64_t dim, const float* norm_w, float eps,
+                           int centered, void* out, int out_dtype, int64_t ldo, void* stream) {
+  if (!x || !norm_w || !out) return fail(FH_EINVAL, "fh_rms_rows: null pointer");
+  if (rows < 1 || dim < 1 || ldx < dim || ldo < dim) return fail(FH_EINVAL, "fh_rms_rows: need rows, dim >= 1, ldx and ldo >= dim");
+  if (out_dtype != FH_F32 && out_dtype != FH_BF16) return fail(FH_EINVAL, "fh_rms_rows: out is FH_F32 or FH_BF16");
+  if (rows >= (1LL << 31)) return fail(FH_EUNSUP, "fh_rms_rows: too many rows");
+  hipStream_t s = as_stream(stream);
+  if (out_dtype == FH_BF16) hipLaunchKernelGGL((rms_rows_kernel<true>), dim3((unsigned)rows), dim3(256), 0, s, x, ldx, (int)dim, norm_w, eps, centered, out, ldo);
+  else hipLaunchKernelGGL((rms_rows_kernel<false>), dim3((unsigned)rows), dim3(256), 0, s, x, ldx, (int)dim, norm_w, eps, centered, out, ldo);
+  return check_launch("fh_rms_rows");
+}

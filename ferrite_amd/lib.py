@@ -38,6 +38,8 @@ SIGNATURES = {
   "fh_embed_rows": ([P, I, L, L, P, I, P, P, P], I),
   "fh_attention_workspace_bytes": ([I, I, I, L], S),
   "fh_attention_decode": ([P, P, I, L, I, I, I, I, P, P, L, P, P, S, P], I),
+  "fh_attention_prefill": ([P, L, P, I, L, I, I, I, I, L, L, P, I, L, P], I),
+  "fh_rms_rows": ([P, L, L, L, P, ctypes.c_float, I, P, I, L, P], I),
   "fh_argmax_rows": ([P, L, L, P, P], I),
   "fh_argmax_parts": ([P, L, L, P, P], I),
 }

@@ -11,6 +11,17 @@ is, per block:
   down    fh_gemv_bfp  + the residual
 then the final norm and the output layer (fp32 logits) and each row's argmax. Activations stay fp32 between
 kernels; weights are block floats (precision's formats); the KV cache is bf16 or fp32.
+
+A prompt (prefill: T tokens at consecutive places of one sequence, models/llama.py:498-504) runs on the matrix cores,
+the residual stream fp32 and each GEMM's input bf16 (as ferrite's chip feeds its matrix unit), per block:
+  norm    fh_rms_rows  x -> bf16 rows
+  qkv     fh_gemm_bfp  RoPE on q's and k's heads, k and v put into the cache at each row's place
+  attend  fh_attention_prefill, causal over the sequence's rows (bf16 out)
+  o       fh_gemm_bfp  + the residual
+  norm    fh_rms_rows
+  gate_up fh_gemm_bfp  silu(gate) * up (bf16 out)
+  down    fh_gemm_bfp  + the residual, with x's sums of squares
+then the final norm and the output layer for the last row only (fh_gemv_bfp), and its argmax.
 """
 import math
 from types import SimpleNamespace
@@ -149,6 +160,57 @@ class Decoder:
     ep = ops.epilogue(lib.EP_STORE, norm_w=self.norm, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered), argmax_parts=self.parts)
     ops.gemv(self.x, self.head, ep, out=self.logits)
     ops.argmax_parts(self.parts, self.picks)
+
+  def _prefill_buffers(self, T):
+    c, hd, dev = self.c, self.hd, self.device
+    P = getattr(self, "_pre", None)
+    if P is None or P.T < T:
+      z = lambda *s, dtype=torch.float32: torch.zeros(*s, dtype=dtype, device=dev)
+      P = SimpleNamespace(T=T, ids=z(T, dtype=torch.int32), places=z(T, dtype=torch.int32), rows=z(T, dtype=torch.int32),
+                          x=z(T, c.dim), ssq=z(T, c.dim // 16), xn=z(T, c.dim, dtype=torch.bfloat16), q=z(T, c.heads * hd),
+                          att=z(T, c.heads * hd, dtype=torch.bfloat16), h=z(T, c.ffn, dtype=torch.bfloat16),
+                          logits=z(1, c.vocab), parts=z(1, c.vocab // 16, dtype=torch.int64), pick=z(1, dtype=torch.int32))
+      self._pre = P
+    return P
+
+  def prefill(self, ids, slot=0, p0=0, chunk=None):
+    """A prompt's tokens at places p0 .. p0 + len(ids) - 1 of sequence `slot`, on the matrix cores (in chunks of
+    `chunk` tokens, as models/llama.py:498-504 prefills): their keys and values go into the cache; returns the last
+    token's logits ([1][vocab] fp32) and its greedy pick ([1] int32)."""
+    ids = [int(i) for i in ids]
+    T = len(ids)
+    if T < 1 or p0 < 0 or p0 + T > min(self.context, self.c.places): raise ValueError("prefill: the prompt's places past the cache or RoPE's tables")
+    chunk = chunk or T
+    for a in range(0, T, chunk):
+      out = self._prefill_chunk(ids[a:a + chunk], slot, p0 + a)
+    return out
+
+  def _prefill_chunk(self, ids, slot, p0):
+    c, hd = self.c, self.hd
+    T = len(ids)
+    P = self._prefill_buffers(T)
+    ids_t, places, rows = P.ids[:T], P.places[:T], P.rows[:T]
+    x, ssq, xn, q, att, h = P.x[:T], P.ssq[:T], P.xn[:T], P.q[:T], P.att[:T], P.h[:T]
+    ids_t.copy_(torch.as_tensor(ids, dtype=torch.int32))
+    places.copy_(torch.arange(p0, p0 + T, dtype=torch.int32))
+    rows.copy_(places + slot * self.part)
+    cache_dtype = lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"]
+    ops.embed_rows(self.embed, ids_t, x, ssq)
+    for l, L in enumerate(self.layers):
+      ops.rms_rows(x, L.norm1, c.eps, c.centered, out=xn)
+      ep = ops.epilogue(lib.EP_ROPE_KV, heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
+                        places=places, cache_rows=rows, cache=self.cache[l], cache_dtype=cache_dtype,
+                        cache_len=self.cache[l].shape[1])
+      ops.gemm(xn, L.qkv, ep, out=q)
+      ops.attention_prefill(q, self.cache[l], c.heads, c.kv, hd, p0, slot * self.part, o=att)
+      ops.gemm(att, L.o, ops.epilogue(lib.EP_RESIDUAL, residual=x), out=x)
+      ops.rms_rows(x, L.norm2, c.eps, c.centered, out=xn)
+      ops.gemm(xn, L.gate_up, ops.epilogue(lib.EP_SILU_GATE, split=c.ffn), out=h)
+      ops.gemm(h, L.down, ops.epilogue(lib.EP_RESIDUAL, residual=x, ssq_out=ssq), out=x)
+    ep = ops.epilogue(lib.EP_STORE, norm_w=self.norm, ssq_in=ssq[T - 1:], eps=c.eps, centered=int(c.centered), argmax_parts=P.parts)
+    ops.gemv(x[T - 1:], self.head, ep, out=P.logits)
+    ops.argmax_parts(P.parts, P.pick)
+    return P.logits, P.pick
 
   def step(self, ids=None, places=None, slots=None, replay=True):
     """One step: the logits (fp32, [batch][vocab]) and picks for tokens ids at places. With replay, the step runs as

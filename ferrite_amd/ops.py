@@ -124,6 +124,28 @@ def attention_decode(q, cache, heads, kv_heads, head_dim, places, first_row, max
   return o
 
 
+def attention_prefill(q, cache, heads, kv_heads, head_dim, p0, slot_row, o=None, out_dtype=torch.float32):
+  """A prompt's causal attention (fh_attention_prefill): q [T][heads*hd] at places p0 .. p0 + T - 1 of the sequence
+  whose cache rows start at slot_row; cache [2 kv][len][hd]."""
+  _dev(q, cache)
+  T = q.shape[0]
+  if o is None: o = torch.empty(T, heads * head_dim, dtype=out_dtype, device=q.device)
+  _dev(o)
+  lib.call("fh_attention_prefill", _ptr(q), q.stride(0), _ptr(cache), _TORCH[cache.dtype], cache.shape[1], T, heads,
+           kv_heads, head_dim, p0, slot_row, _ptr(o), _TORCH[o.dtype], o.stride(0), _stream())
+  return o
+
+
+def rms_rows(x, w, eps, centered=False, out=None, out_dtype=torch.bfloat16):
+  """x * rsqrt(mean(x^2) + eps) * w, a row at a time (fh_rms_rows); bf16 out by default (a prefill GEMM's input)."""
+  _dev(x, w)
+  if out is None: out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+  _dev(out)
+  lib.call("fh_rms_rows", _ptr(x), x.stride(0), x.shape[0], x.shape[1], _ptr(w), eps, int(centered), _ptr(out),
+           _TORCH[out.dtype], out.stride(0), _stream())
+  return out
+
+
 def argmax_rows(x, ids=None):
   _dev(x)
   if ids is None: ids = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)

@@ -143,6 +143,21 @@ int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int6
                         int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row, int64_t max_context,
                         float* o, void* workspace, size_t ws_bytes, void* stream);
 
+/* A prompt's causal attention (models/llama.py:129-142 over a chunk of consecutive places; prefill, 498-504): rows
+ * t = 0 .. T-1 of q [T][ldq] (fp32) are places p0 + t of the sequence whose cache rows start at slot_row; row t
+ * attends to cache rows slot_row .. slot_row + p0 + t, which must already hold its keys and values (the qkv GEMM's
+ * FH_EP_ROPE_KV put them there). On the matrix cores: q, k, v and the softmax weights in bf16, scores and sums fp32;
+ * head_dim 64 or 128. o: [T][ldo], fp32 or bf16 (for the next GEMM). No scratch memory. Replaces Tensor.attend's
+ * prompt path (ferrite/tensor.py:487-516; attention_kernel, ferrite/compiler.py:1147-1316). */
+int fh_attention_prefill(const float* q, int64_t ldq, const void* cache, int cache_dtype, int64_t cache_len, int T,
+                         int heads, int kv_heads, int head_dim, int64_t p0, int64_t slot_row, void* o, int o_dtype,
+                         int64_t ldo, void* stream);
+
+/* out[rows][dim] = x * rsqrt(mean(x^2) + eps) * w (w + 1 when centered), fp32 or bf16 out: the RMSNorm before a
+ * prefill GEMM (models/llama.py:82-85), which then takes bf16 rows. */
+int fh_rms_rows(const float* x, int64_t ldx, int64_t rows, int64_t dim, const float* norm_w, float eps, int centered,
+                void* out, int out_dtype, int64_t ldo, void* stream);
+
 /* For each row of x[rows][n] (fp32), its largest value's column (the first of equals), into ids[rows]: greedy
  * decoding's pick (models/llama.py:792, numpy's argmax). */
 int fh_argmax_rows(const float* x, int64_t rows, int64_t n, int32_t* ids, void* stream);
