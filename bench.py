@@ -1,13 +1,13 @@
 """The hot path's benchmark: ferrite's block-float decode on one MI355X, on the 8B decode workload (Llama-3.1-8B's shape,
 attention and the output layer in bfp8, every MLP matrix in bfp4, a bf16 KV cache at context 2048, batch 1).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c3-bfp8|c2] [--batch B] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c3-bfp8|c2] [--batch B] [--no-cpu] [--no-prefill]
 
 Prints ONE JSON line: tokens/s of the whole decode step (every kernel of it replayed as one HIP graph, inputs resident
 in HBM), the dominant GEMV's achieved HBM bandwidth against the 8 TB/s peak (timed live with HIP events on its own
 stream), each GEMV's GB/s, and the CPU baseline: the numpy restatement (oracle/) of one block and the output layer
-timed on this host's cores and scaled to a token. Synthetic data: random-init weights, drawn on the GPU and packed
-there."""
+timed on this host's cores and scaled to a token; and config 4's prefill (a 2048-token prompt on the matrix cores) as
+its own field. Synthetic data: random-init weights, drawn on the GPU and packed there."""
 import argparse, json, os, statistics, sys, time
 import numpy as np
 import torch
@@ -16,6 +16,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s (published)
+MFMA_PEAK = 2.5e15  # MI355X dense bf16 matrix-core FLOP/s (published)
 
 
 def config(name):
@@ -82,6 +83,56 @@ def gemv_rates(dec, stream, reps=5):
   return out
 
 
+def prefill_rate(T=2048, reps=3):
+  """Config 4: a T-token prompt through the 8B shape with every matrix bfp8 (the matrix-core path: fh_rms_rows,
+  fh_gemm_bfp, fh_attention_prefill; the output layer on the last token), timed by HIP events on its stream; and each
+  GEMM shape and the attention alone. FLOPs are the algorithmic ones: 2 T K N a matmul, 4 hd heads T(T+1)/2 a
+  block's causal attention, 2 dim vocab the last token's output layer."""
+  from ferrite_amd import llama as G, ops
+  c, _, _ = config("c3")
+  dev = torch.device("cuda:0")
+  dec = G.Decoder(c, G.random_weights(c, seed=2, device=dev), mode="bfp8", kv="bf16", batch=1, context=T)
+  hd = dec.hd
+  ids = [(7 * i + 3) % c.vocab for i in range(T)]
+  stream = torch.cuda.Stream(device=dev)
+  mats = {"qkv": (c.dim, dec.qkv_cols), "o": (c.heads * hd, c.dim), "gate_up": (c.dim, 2 * c.ffn), "down": (c.ffn, c.dim)}
+  lin = sum(2 * T * k * n for k, n in mats.values()) * c.layers
+  att = 4 * hd * c.heads * T * (T + 1) // 2 * c.layers
+  flops = lin + att + 2 * c.dim * c.vocab
+  def timed(fn, n):
+    with torch.cuda.stream(stream):
+      fn()
+      torch.cuda.synchronize()
+      a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+      a.record(stream)
+      for _ in range(n): fn()
+      b.record(stream)
+      b.synchronize()
+    return a.elapsed_time(b) / n
+  ms = timed(lambda: dec.prefill(ids), reps)
+  out = {"workload": f"config 4: Llama-3.1-8B-shape prefill of {T} tokens, all bfp8, bf16 KV", "ms": round(ms, 3),
+         "tokens_per_s": round(T * 1000 / ms, 1), "tflops": round(flops / ms / 1e9, 1),
+         "mfma_frac": round(flops / ms * 1e3 / MFMA_PEAK, 4), "flops": flops}
+  L = dec.layers[0]
+  xb = torch.randn(T, max(c.dim, c.ffn), device=dev).to(torch.bfloat16)
+  P = dec._prefill_buffers(T)
+  shapes = {"qkv": (L.qkv, xb[:, :c.dim], torch.empty(T, dec.qkv_cols, device=dev)),
+            "o": (L.o, xb[:, :c.dim], torch.empty(T, c.dim, device=dev)),
+            "gate_up": (L.gate_up, xb[:, :c.dim], torch.empty(T, 2 * c.ffn, device=dev)),
+            "down": (L.down, xb[:, :c.ffn], torch.empty(T, c.dim, device=dev))}
+  g = {}
+  for name, (w, x, y) in shapes.items():
+    x = x.contiguous()
+    t = timed(lambda: ops.gemm(x, w, out=y), 5)
+    g[name] = round(2 * T * w.K * w.N / t / 1e9, 1)
+  t = timed(lambda: ops.attention_prefill(P.q[:T], dec.cache[0], c.heads, c.kv, hd, 0, 0, o=P.att[:T]), 5)
+  out["gemm_tflops"] = g
+  out["attention_tflops"] = round(4 * hd * c.heads * T * (T + 1) / 2 / t / 1e9, 1)
+  del dec
+  torch.cuda.empty_cache()
+  return out
+
+
 def measured_traffic(kernel, config, batch):
   """HBM bytes a launch of `kernel` moves, as the committed rocprofv3 counter summaries under profiles/ record them
   (lines `traffic: <kernel> <config> b<batch> <bytes>`: FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's
@@ -141,6 +192,7 @@ def main():
   ap.add_argument("--config", default="c3")
   ap.add_argument("--batch", type=int, default=1)
   ap.add_argument("--no-cpu", action="store_true")
+  ap.add_argument("--no-prefill", action="store_true", help="skip config 4's prefill measurement")
   ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                   help="first run a plain copy kernel (torch.neg) over MIB MiB: the known-size kernel that calibrates "
                        "rocprofv3's FETCH_SIZE/WRITE_SIZE counters in the same run")
@@ -191,6 +243,12 @@ def main():
   dom = max(rates, key=lambda k: rates[k]["us"] * (c.layers if k != "head" else 1))  # the most time in a step
   r = rates[dom]
   epi = {"qkv": "RMSNorm+RoPE+KV put", "o": "residual", "gate_up": "RMSNorm+SiLU*gate", "down": "residual", "head": "RMSNorm+argmax"}
+  pre = None
+  if not args.no_prefill and args.config == "c3":
+    pre = prefill_rate()
+    print(f"# prefill {pre['workload']}: {pre['ms']:.1f} ms, {pre['tokens_per_s']:.0f} tok/s, {pre['tflops']:.0f} TFLOP/s "
+          f"({pre['mfma_frac']:.1%} of {MFMA_PEAK / 1e15:.1f} PFLOP/s); gemm {pre['gemm_tflops']}, attention {pre['attention_tflops']} TFLOP/s",
+          file=sys.stderr, flush=True)
   cpu = None
   if not args.no_cpu:
     cpu = cpu_baseline(c, mode, context)
@@ -211,6 +269,7 @@ def main():
     "gemv_gbs": {k: round(v["gbs"], 1) for k, v in rates.items()},
     "gemv_us": {k: round(v["us"], 3) for k, v in rates.items()},
     "cpu_baseline": cpu,
+    "prefill": pre,
   }
   print(json.dumps(line), flush=True)
 
