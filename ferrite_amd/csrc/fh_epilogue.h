@@ -72,6 +72,19 @@ __device__ inline void magnitudes8(const uint32_t& m, float (&f)[8]) {
 // RoPE, where half = head_dim / 32; gate and up for SiLU·gate, where half = split / 16 and there is one group).
 __host__ __device__ inline int64_t pair_first(int64_t item, int half) { return item / half * (2 * half) + item % half; }
 
+// A grouped (mixture-of-experts) skinny matmul's extras (fh_skinny.hip): grid.y = expert, its weight `expert_mant` /
+// `expert_exps` bytes on and its outputs `expert_cols` columns on, each row's output scaled by row_scale[row][expert];
+// or, with k_expert > 0, W is the experts stacked along K (k_expert rows each) and only the steps of experts some row
+// picked (row_scale not 0) are read.
+struct SkinnyMoe {
+  int64_t expert_mant, expert_exps, expert_cols;
+  const float* row_scale; int experts;
+  int64_t k_expert;
+};
+
+// x @ W for up to 64 rows a pass on the matrix cores (fh_skinny.hip); a's epilogue already checked
+int skinny_matmul(const MatArgs& a, const SkinnyMoe& moe, int fmt, int experts, hipStream_t s);
+
 // Checks an fh_epilogue against the matmul's shape and fills a's prologue and epilogue fields (x, weight and y
 // fields are the caller's). `who` names the entry point in messages.
 inline int epilogue_args(const char* who, const fh_epilogue* ep, int64_t K, int64_t N, int y_dtype, int64_t ldy, MatArgs& a) {

@@ -307,11 +307,15 @@ extern "C" int fh_gemm_bfp(const void* x, int x_dtype, int64_t ldx, int64_t M, i
   a.mant = (const uint8_t*)w_mant; a.exps = w_exps; a.K = K; a.N = N; a.M = M;
   a.y = y; a.y_bf16 = y_dtype == FH_BF16; a.ldy = ldy;
   if (int rc = epilogue_args("fh_gemm_bfp", ep, K, N, y_dtype, ldy, a)) return rc;
+  hipStream_t s = as_stream(stream);
+  if (M <= 64 && K % 64 == 0) {  // a few rows: the skinny kernel (K split among waves, as the GEMV splits it)
+    const SkinnyMoe none = {};
+    return skinny_matmul(a, none, fmt, 1, s);
+  }
   const int64_t tiles_m = (M + GM_BM - 1) / GM_BM;
   const int64_t tiles_n = a.P == 1 ? (N / 16 + 7) / 8 : ((int64_t)a.items + 3) / 4;
   if (tiles_m * tiles_n >= (1LL << 31)) return fail(FH_EUNSUP, "fh_gemm_bfp: too many tiles");
   const dim3 g((unsigned)(tiles_m * tiles_n)), b(GM_THREADS);
-  hipStream_t s = as_stream(stream);
   const int tm = (int)tiles_m, tn = (int)tiles_n;
   const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
   switch (which) {

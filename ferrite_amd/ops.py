@@ -146,6 +146,53 @@ def rms_rows(x, w, eps, centered=False, out=None, out_dtype=torch.bfloat16):
   return out
 
 
+def moe_route(x, router, experts, k, norm_topk=True, norm_w=None, eps=1e-5, centered=False):
+  """Router logits, top k and their weights (fh_moe_route): (ids [rows][k] int32, weights [rows][k], dense [rows][E])."""
+  _dev(x, router, norm_w)
+  rows, dim = x.shape
+  ids = torch.empty(rows, k, dtype=torch.int32, device=x.device)
+  wts = torch.empty(rows, k, dtype=torch.float32, device=x.device)
+  dense = torch.empty(rows, experts, dtype=torch.float32, device=x.device)
+  lib.call("fh_moe_route", _ptr(x), x.stride(0), rows, dim, _ptr(norm_w), eps, int(centered), _ptr(router),
+           _TORCH[router.dtype], experts, k, int(norm_topk), _ptr(ids), _ptr(wts), _ptr(dense), _stream())
+  return ids, wts, dense
+
+
+@dataclass
+class Experts:
+  """A mixture of experts' weights on the GPU: gate_up, the experts' [dim][2 ffn] packed one after another; down, the
+  experts' [ffn][dim] stacked into one [experts * ffn][dim] matrix, packed."""
+  gate_up: BfpWeight
+  down: BfpWeight
+  experts: int
+  dim: int
+  ffn: int
+
+
+def pack_experts(gate_up, down, fmt="bfp4"):
+  """gate_up [E][dim][2 ffn] and down [E][ffn][dim] (fp32 or bf16, on the GPU) as block floats (fh_bfp_pack)."""
+  E, dim, two = gate_up.shape
+  ffn = two // 2
+  parts = [pack(gate_up[e], fmt) for e in range(E)]
+  gu = BfpWeight(torch.cat([p.mant for p in parts]), torch.cat([p.exps for p in parts]), dim, 2 * ffn, fmt)
+  dn = pack(down.reshape(E * ffn, dim), fmt)
+  return Experts(gu, dn, E, dim, ffn)
+
+
+def moe_experts(x, ex, dense, out=None, residual=None, ssq_out=None, norm_w=None, ssq_in=None, eps=1e-5, centered=False, ws=None):
+  """The picked experts' SwiGLUs weighted by dense and summed, plus residual (fh_moe_experts). x [rows][dim] fp32."""
+  _dev(x, dense, out, residual, ssq_out, norm_w, ssq_in)
+  rows = x.shape[0]
+  if out is None: out = torch.empty(rows, ex.dim, dtype=torch.float32, device=x.device)
+  n = lib.load().fh_moe_workspace_bytes(rows, ex.experts, ex.ffn)
+  if ws is None or ws.numel() < n: ws = torch.empty(max(n, 256), dtype=torch.uint8, device=x.device)
+  lib.call("fh_moe_experts", _ptr(x), x.stride(0), rows, ex.dim, _ptr(norm_w), _ptr(ssq_in), eps, int(centered),
+           ex.experts, ex.ffn, _ptr(ex.gate_up.mant), _ptr(ex.gate_up.exps), lib.DTYPES[ex.gate_up.fmt], _ptr(ex.down.mant),
+           _ptr(ex.down.exps), lib.DTYPES[ex.down.fmt], _ptr(dense), _ptr(out), _ptr(residual), _ptr(ssq_out), _ptr(ws),
+           ws.numel(), _stream())
+  return out
+
+
 def argmax_rows(x, ids=None):
   _dev(x)
   if ids is None: ids = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)

@@ -120,7 +120,9 @@ int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, int64_t K, i
  * RMSNorm weight) is rounded to bf16 (nearest even), the weight's values are exact. Every epilogue of fh_gemv_bfp,
  * with [M] in place of [batch] (FH_EP_ROPE_KV: each row its own place and cache row, a prompt's tokens at once).
  * Replaces fused_kernel's matmul for prompt rows (ferrite/compiler.py:699-1111 over 32-row tiles; models/llama.py's
- * prefill, 498-504). No scratch memory; results do not depend on timing. */
+ * prefill, 498-504). Up to 64 rows with K a multiple of 64 (a decode step of many sequences) take a kernel that splits
+ * K among a workgroup's waves as the GEMV does; more rows take 128 x 128 tiles. No scratch memory; results do not
+ * depend on timing. */
 int fh_gemm_bfp(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int64_t N, const void* w_mant,
                 const uint8_t* w_exps, int fmt, const fh_epilogue* ep, void* y, int y_dtype, int64_t ldy, void* stream);
 
@@ -157,6 +159,30 @@ int fh_attention_prefill(const float* q, int64_t ldq, const void* cache, int cac
  * prefill GEMM (models/llama.py:82-85), which then takes bf16 rows. */
 int fh_rms_rows(const float* x, int64_t ldx, int64_t rows, int64_t dim, const float* norm_w, float eps, int centered,
                 void* out, int out_dtype, int64_t ldo, void* stream);
+
+/* ---- mixture of experts (models/llama.py:277-329) ------------------------------------------------------------ */
+
+/* Each row of x [rows][ldx] (fp32; RMSNorm'd first when norm_w is given, by its own sums of squares): the router's
+ * logits x @ router (router [dim][experts], bf16 or fp32; fp32 sums), the k largest (the first of equals first:
+ * numpy's stable argsort, models/llama.py:27; Tensor.topk, ferrite/tensor.py:373-388) and their weights: a softmax
+ * over the k (norm_topk), or the softmax over all experts at the k. Out: ids [rows][k] int32, weights [rows][k] fp32,
+ * and dense [rows][experts] fp32 (each row's weight for each expert, 0 where not picked; Tensor.touched's weights,
+ * ferrite/tensor.py:403-416). experts <= 256, k <= 16. */
+int fh_moe_route(const float* x, int64_t ldx, int rows, int64_t dim, const float* norm_w, float eps, int centered,
+                 const void* router, int router_dtype, int experts, int k, int norm_topk, int32_t* ids, float* weights,
+                 float* dense, void* stream);
+
+/* The chosen experts' SwiGLUs, weighted and summed (numpy_experts / chip_experts' dense path, models/llama.py:294-321):
+ * y = residual + sum_e dense[:, e] * (silu(h @ gate_e) * (h @ up_e)) @ down_e, h = x with the RMSNorm prologue
+ * (norm_w, ssq_in as fh_gemv_bfp's). gate_up: the experts' [dim][2 ffn] weights packed one after another (FH_AXIS_N);
+ * down: the experts' [ffn][dim] weights stacked into one [experts * ffn][dim] matrix, packed. An expert no row picked
+ * reads no weight. residual NULL: y is the sum alone; ssq_out: y's sums of squares by 16 columns. On the matrix
+ * cores, x in bf16 (fh_gemm_bfp's arithmetic). Workspace: fh_moe_workspace_bytes (the gate_up outputs of 64 rows). */
+size_t fh_moe_workspace_bytes(int rows, int experts, int64_t ffn);
+int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim, const float* norm_w, const float* ssq_in, float eps,
+                   int centered, int experts, int64_t ffn, const void* gu_mant, const uint8_t* gu_exps, int gu_fmt,
+                   const void* down_mant, const uint8_t* down_exps, int down_fmt, const float* dense, float* y,
+                   const float* residual, float* ssq_out, void* workspace, size_t ws_bytes, void* stream);
 
 /* For each row of x[rows][n] (fp32), its largest value's column (the first of equals), into ids[rows]: greedy
  * decoding's pick (models/llama.py:792, numpy's argmax). */

@@ -47,7 +47,10 @@ def within(got, want, bound, what):
 def test_gemm_shapes(cuda, fmt):
   # row counts around the 128-row tile, N not a multiple of the 128-column tile, K not a multiple of the 64-row step
   rng = np.random.default_rng(11)
-  for M, K, N in ((1, 64, 16), (5, 576, 960), (128, 1536, 576), (200, 96, 2064), (300, 4096, 256)):
+  # (up to 64 rows with K a multiple of 64 take the skinny kernel: K split among a workgroup's waves; 3 runs of 16
+  # leave its last item one run)
+  for M, K, N in ((1, 64, 16), (5, 576, 960), (33, 64, 48), (64, 1536, 576), (16, 4096, 1024), (128, 1536, 576),
+                  (200, 96, 2064), (300, 4096, 256)):
     w = wide(rng, (K, N)) * 0.02
     bw = ops().pack(to_gpu(w), fmt)
     wv = O.bfp(w, fmt)
@@ -83,12 +86,13 @@ def test_gemm_rejects(cuda):
     ops().gemm(to_gpu(np.ones((2, 48), np.float32)), w)
 
 
-def test_gemm_epilogues(cuda):
-  # every epilogue over a prompt's rows, each row its own place (models/llama.py's prefill, 498-504)
+@pytest.mark.parametrize("M", [150, 37, 16])
+def test_gemm_epilogues(cuda, M):
+  # every epilogue over a prompt's rows (150: the tiled kernel), or a decode step of many sequences (37, 16: the
+  # skinny one), each row its own place (models/llama.py's prefill, 498-504)
   L = lib()
   rng = np.random.default_rng(13)
   c = OL.model(dim=576, heads=9, kv=3, layers=1, eps=1e-5, theta=10000.0, ffn=1536, places=256)
-  M = 150
   x = rng.normal(0, 1, (M, c.dim)).astype(np.float32)
   g = O.bf16(rng.normal(1, 0.1, (1, c.dim)))
   ssq = (x.reshape(M, -1, 16).astype(np.float32) ** 2).sum(-1)
