@@ -133,6 +133,70 @@ def prefill_rate(T=2048, reps=3):
   return out
 
 
+def decode_batch(dec, context, B=16, steps=20):
+  """Config 3 at batch 16: 16 sequences a step, each at the last place of a full context of its own (a slot of the
+  cache each), the matmuls on the matrix cores (the skinny kernel), the step replayed as a HIP graph; the weights are
+  the batch-1 decoder's."""
+  from ferrite_amd import llama as G
+  c = dec.c
+  d = G.Decoder(c, None, mode=dec.mode, kv="bf16", batch=B, context=context, slots=B, share=dec)
+  for cache in d.cache: cache.normal_(0, 1)
+  stream = torch.cuda.Stream()
+  with torch.cuda.stream(stream):
+    d.ids.copy_(torch.arange(B, dtype=torch.int32) * 7 + 1)
+    d.set_rows([context - 1] * B, list(range(B)))
+    d.step(replay=True)
+    for _ in range(3): d.graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps): d.graph.replay()
+    b.record(stream)
+    b.synchronize()
+  ms = a.elapsed_time(b) / steps
+  kv = c.layers * 2 * c.kv * d.hd * context * 2 * B
+  nbytes = d.weight_bytes() + kv
+  out = {"workload": f"config 3 at batch {B}: {B} sequences at context {context}, matmuls on the matrix cores",
+         "batch": B, "ms_per_step": round(ms, 4), "tokens_per_s": round(B * 1000 / ms, 1),
+         "step_gbs": round(nbytes / ms / 1e6, 1)}
+  del d
+  torch.cuda.empty_cache()
+  return out
+
+
+def moe_rate(T=32, reps=20):
+  """Config 5: a Mixtral-shape mixture-of-experts layer for T tokens: h [T][4096] ~N(0,1) bf16 values, router
+  [4096][8] bf16 ~N(0, 0.02), 8 experts' gate_up [4096][28672] and down [14336][4096] ~N(0, 0.02) in bfp4, top 2
+  (fh_moe_route, fh_moe_experts), timed as one HIP graph by events. Bytes: the experts some token picked, each read
+  once, the router, h and the output."""
+  from ferrite_amd import ops
+  dev = torch.device("cuda:0")
+  dim, ffn, E, k = 4096, 14336, 8, 2
+  g = torch.Generator(device=dev)
+  g.manual_seed(5)
+  h = torch.randn(T, dim, generator=g, device=dev).to(torch.bfloat16).float()
+  router = (torch.randn(dim, E, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+  gu = (torch.randn(E, dim, 2 * ffn, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+  dn = (torch.randn(E, ffn, dim, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+  ex = ops.pack_experts(gu, dn, "bfp4")
+  del gu, dn
+  torch.cuda.empty_cache()
+  y = torch.empty(T, dim, device=dev)
+  ws = torch.empty(max(ops.lib.load().fh_moe_workspace_bytes(T, E, ffn, dim), 256), dtype=torch.uint8, device=dev)
+  state = {}
+  def run():
+    ids, w, dense = ops.moe_route(h, router, E, k)
+    state["dense"] = dense
+    ops.moe_experts(h, ex, dense, out=y, ws=ws)
+  stream = torch.cuda.Stream(device=dev)
+  ms = timed_graph(run, reps, stream)
+  touched = int((state["dense"] != 0).any(0).sum())
+  nbytes = touched * (ex.gate_up.nbytes + ex.down.nbytes) // E + dim * E * 2 + T * dim * 4 * 2
+  return {"workload": f"config 5: Mixtral-shape MoE layer, {T} tokens, {E} experts bfp4, top {k}", "us": round(ms * 1e3, 2),
+          "experts_touched": touched, "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+          "frac": round(nbytes / ms * 1e3 / HBM_PEAK, 4)}
+
+
 def measured_traffic(kernel, config, batch):
   """HBM bytes a launch of `kernel` moves, as the committed rocprofv3 counter summaries under profiles/ record them
   (lines `traffic: <kernel> <config> b<batch> <bytes>`: FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's
@@ -243,6 +307,14 @@ def main():
   dom = max(rates, key=lambda k: rates[k]["us"] * (c.layers if k != "head" else 1))  # the most time in a step
   r = rates[dom]
   epi = {"qkv": "RMSNorm+RoPE+KV put", "o": "residual", "gate_up": "RMSNorm+SiLU*gate", "down": "residual", "head": "RMSNorm+argmax"}
+  extra = {}
+  if args.config == "c3" and B == 1 and not args.no_prefill:
+    extra["decode_bs16"] = decode_batch(dec, context)
+    print(f"# {extra['decode_bs16']['workload']}: {extra['decode_bs16']['ms_per_step']:.3f} ms, "
+          f"{extra['decode_bs16']['tokens_per_s']:.0f} tok/s, {extra['decode_bs16']['step_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    extra["moe"] = moe_rate()
+    print(f"# {extra['moe']['workload']}: {extra['moe']['us']:.1f} us, {extra['moe']['gbs']:.0f} GB/s "
+          f"({extra['moe']['frac']:.1%}), {extra['moe']['experts_touched']} experts touched", file=sys.stderr, flush=True)
   pre = None
   if not args.no_prefill and args.config == "c3":
     pre = prefill_rate()
@@ -270,6 +342,7 @@ def main():
     "gemv_us": {k: round(v["us"], 3) for k, v in rates.items()},
     "cpu_baseline": cpu,
     "prefill": pre,
+    **extra,
   }
   print(json.dumps(line), flush=True)
 

@@ -73,13 +73,13 @@ __device__ inline void magnitudes8(const uint32_t& m, float (&f)[8]) {
 __host__ __device__ inline int64_t pair_first(int64_t item, int half) { return item / half * (2 * half) + item % half; }
 
 // A grouped (mixture-of-experts) skinny matmul's extras (fh_skinny.hip): grid.y = expert, its weight `expert_mant` /
-// `expert_exps` bytes on and its outputs `expert_cols` columns on, each row's output scaled by row_scale[row][expert];
-// or, with k_expert > 0, W is the experts stacked along K (k_expert rows each) and only the steps of experts some row
-// picked (row_scale not 0) are read.
+// `expert_exps` bytes on and its outputs `expert_cols` columns on; an expert whose row_scale[.][expert] are all 0 reads
+// nothing; with scale_rows, each row's output is scaled by row_scale[row][expert]; expert e's x starts expert_xcols * e
+// columns into x's rows.
 struct SkinnyMoe {
-  int64_t expert_mant, expert_exps, expert_cols;
+  int64_t expert_mant, expert_exps, expert_cols, expert_xcols;
   const float* row_scale; int experts;
-  int64_t k_expert;
+  int scale_rows;
 };
 
 // x @ W for up to 64 rows a pass on the matrix cores (fh_skinny.hip); a's epilogue already checked

@@ -9,9 +9,10 @@
 //
 // fh_moe_experts: ferrite's dense path for a decode step's few tokens (Tensor.touched, chip_experts: every expert some
 // row picked takes every row, weighted by each row's weight, 0 where it did not pick it; llama.py:302-321): the skinny
-// matrix-core kernel over (expert, 32 columns) for gate_up with the SiLU·gate epilogue scaled by the row's weight into
-// a [rows][experts * ffn] bf16 workspace, then down as one matrix of the experts stacked along K (the weighted sum over
-// experts is the sum over K), skipping the K steps of experts no row picked, with the residual epilogue.
+// matrix-core kernel over (32 columns, expert) for gate_up with the SiLU·gate epilogue scaled by the row's weight into
+// a [rows][experts * ffn] bf16 workspace, then for down into [rows][experts * dim] fp32, and a last kernel sums the
+// experts in expert order (no atomics: the result does not depend on timing) onto the residual. An expert no row
+// picked reads no weight and leaves zeros.
 #include <math.h>
 #include "fh_epilogue.h"
 
@@ -103,6 +104,26 @@ __global__ __launch_bounds__(RT_THREADS) void route_kernel(const float* x, int64
   }
 }
 
+// y[row] = residual[row] + the experts' outputs summed in expert order, and y's sums of squares by 16 columns
+__global__ __launch_bounds__(256) void moe_sum_kernel(const float* parts, int experts, int dim, const float* residual,
+                                                      float* y, float* ssq_out) {
+  const int64_t row = blockIdx.x;
+  for (int n0 = 0; n0 < dim; n0 += 256) {
+    const int n = n0 + threadIdx.x;
+    float v = 0.f;
+    if (n < dim) {
+      v = residual ? residual[row * dim + n] : 0.f;
+      for (int e = 0; e < experts; ++e) v += parts[(row * experts + e) * dim + n];
+      y[row * dim + n] = v;
+    }
+    if (ssq_out) {  // (dim is a multiple of 64: a run of 16 is 16 neighbouring lanes, all in range)
+      float s = v * v;
+      s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
+      if (n < dim && (n & 15) == 0) ssq_out[row * (dim / 16) + n / 16] = s;
+    }
+  }
+}
+
 }  // namespace fh
 
 using namespace fh;
@@ -125,9 +146,9 @@ extern "C" int fh_moe_route(const float* x, int64_t ldx, int rows, int64_t dim, 
   return check_launch("fh_moe_route");
 }
 
-extern "C" size_t fh_moe_workspace_bytes(int rows, int experts, int64_t ffn) {
-  const int64_t r = rows < 64 ? rows : 64;
-  return (size_t)(r > 0 ? r : 0) * experts * ffn * 2;
+extern "C" size_t fh_moe_workspace_bytes(int rows, int experts, int64_t ffn, int64_t dim) {
+  const int64_t r = rows < 64 ? rows : 64;  // a pass: its gate_up outputs (bf16) and its experts' down outputs (fp32)
+  return (size_t)(r > 0 ? r : 0) * experts * (ffn * 2 + dim * 4);
 }
 
 extern "C" int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim, const float* norm_w, const float* ssq_in,
@@ -141,41 +162,48 @@ extern "C" int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim
   if (experts < 1 || experts > 256) return fail(FH_EUNSUP, "fh_moe_experts: at most 256 experts");
   if ((gu_fmt != FH_BFP8 && gu_fmt != FH_BFP4) || (down_fmt != FH_BFP8 && down_fmt != FH_BFP4)) return fail(FH_EINVAL, "fh_moe_experts: weights are FH_BFP8 or FH_BFP4");
   if (norm_w && !ssq_in) return fail(FH_EINVAL, "fh_moe_experts: the RMSNorm prologue needs ssq_in");
-  if (ws_bytes < fh_moe_workspace_bytes(rows, experts, ffn)) return fail(FH_EINVAL, "fh_moe_experts: workspace too small");
+  if (ws_bytes < fh_moe_workspace_bytes(rows, experts, ffn, dim)) return fail(FH_EINVAL, "fh_moe_experts: workspace too small");
   hipStream_t s = as_stream(stream);
   const int64_t gu_n = 2 * ffn;
   size_t mb, eb;
   if (int rc = fh_bfp_bytes(dim, gu_n, gu_fmt, FH_AXIS_N, &mb, &eb)) return rc;
-  for (int r0 = 0; r0 < rows; r0 += 64) {  // 64 rows a pass (the workspace holds a pass's gate_up outputs)
+  size_t dmb, deb;
+  if (int rc = fh_bfp_bytes(ffn, dim, down_fmt, FH_AXIS_N, &dmb, &deb)) return rc;
+  for (int r0 = 0; r0 < rows; r0 += 64) {  // 64 rows a pass
     const int n = rows - r0 < 64 ? rows - r0 : 64;
-    uint16_t* g = (uint16_t*)workspace;
-    // gate_up of every picked expert: silu(gate) * up * the row's weight, [n][experts * ffn]
+    uint16_t* g = (uint16_t*)workspace;                                   // [n][experts * ffn] bf16
+    float* parts = (float*)((char*)workspace + (size_t)n * experts * ffn * 2);  // [n][experts * dim]
+    // gate_up of every picked expert: silu(gate) * up * the row's weight
     MatArgs a = {};
     fh_epilogue ep = {};
     ep.kind = FH_EP_SILU_GATE; ep.split = (int)ffn; ep.norm_w = norm_w; ep.ssq_in = ssq_in ? ssq_in + (int64_t)r0 * (dim / 16) : nullptr;
     ep.eps = eps; ep.centered = centered;
     a.x = x + (int64_t)r0 * ldx; a.ldx = ldx; a.x_bf16 = 0;
     a.mant = (const uint8_t*)gu_mant; a.exps = gu_exps; a.K = dim; a.N = gu_n; a.M = n;
-    a.y = g; a.ldy = (int64_t)experts * ffn; a.y_bf16 = 1;
+    a.y = g; a.y_bf16 = 1;
     if (int rc = epilogue_args("fh_moe_experts", &ep, dim, gu_n, FH_BF16, ffn, a)) return rc;
     a.ldy = (int64_t)experts * ffn;
     SkinnyMoe moe = {};
     moe.expert_mant = (int64_t)mb; moe.expert_exps = (int64_t)eb; moe.expert_cols = ffn;
-    moe.row_scale = dense + (int64_t)r0 * experts; moe.experts = experts;
+    moe.row_scale = dense + (int64_t)r0 * experts; moe.experts = experts; moe.scale_rows = 1;
     if (int rc = skinny_matmul(a, moe, gu_fmt, experts, s)) return rc;
-    // down: the experts stacked along K, + the residual
+    // down, each picked expert's own outputs
     MatArgs d = {};
     fh_epilogue de = {};
-    de.kind = residual ? FH_EP_RESIDUAL : FH_EP_STORE;
-    de.residual = residual ? residual + (int64_t)r0 * dim : nullptr;
-    de.ssq_out = ssq_out ? ssq_out + (int64_t)r0 * (dim / 16) : nullptr;
+    de.kind = FH_EP_STORE;
     d.x = g; d.ldx = (int64_t)experts * ffn; d.x_bf16 = 1;
-    d.mant = (const uint8_t*)down_mant; d.exps = down_exps; d.K = (int64_t)experts * ffn; d.N = dim; d.M = n;
-    d.y = y + (int64_t)r0 * dim; d.ldy = dim; d.y_bf16 = 0;
-    if (int rc = epilogue_args("fh_moe_experts", &de, d.K, dim, FH_F32, dim, d)) return rc;
+    d.mant = (const uint8_t*)down_mant; d.exps = down_exps; d.K = ffn; d.N = dim; d.M = n;
+    d.y = parts; d.y_bf16 = 0;
+    if (int rc = epilogue_args("fh_moe_experts", &de, ffn, dim, FH_F32, dim, d)) return rc;
+    d.ldy = (int64_t)experts * dim;
     SkinnyMoe dm = {};
-    dm.row_scale = dense + (int64_t)r0 * experts; dm.experts = experts; dm.k_expert = ffn;
-    if (int rc = skinny_matmul(d, dm, down_fmt, 1, s)) return rc;
+    dm.expert_mant = (int64_t)dmb; dm.expert_exps = (int64_t)deb; dm.expert_cols = dim; dm.expert_xcols = ffn;
+    dm.row_scale = dense + (int64_t)r0 * experts; dm.experts = experts; dm.scale_rows = 0;
+    if (int rc = skinny_matmul(d, dm, down_fmt, experts, s)) return rc;
+    hipLaunchKernelGGL(moe_sum_kernel, dim3(n), dim3(256), 0, s, parts, experts, (int)dim,
+                       residual ? residual + (int64_t)r0 * dim : nullptr, y + (int64_t)r0 * dim,
+                       ssq_out ? ssq_out + (int64_t)r0 * (dim / 16) : nullptr);
+    if (int rc = check_launch("fh_moe_experts")) return rc;
   }
   return FH_OK;
 }

@@ -10,10 +10,10 @@
 // 32 x 32 (or 64 x 32) sums then meet in LDS in a fixed order and the epilogue runs on the item's outputs.
 //
 // For a mixture of experts the grid's second dimension is the expert: the weight is the expert's (`expert_mant` /
-// `expert_exps` bytes apart), its outputs go `expert_cols` columns further on, and each row's output is scaled by that
-// row's weight for the expert (0 where the row did not pick it); an expert no row picked reads nothing. With
-// `k_expert` set, W is the experts' matrices stacked along K (expert e's rows e * k_expert ..), and a K step of an
-// expert no row picked is skipped.
+// `expert_exps` bytes apart), its outputs go `expert_cols` columns further on, and (scale_rows) each row's output is
+// scaled by that row's weight for the expert (0 where the row did not pick it); an expert no row picked reads nothing.
+//
+// A wave keeps two steps' loads in flight: each step's loads go out right after the step two before it is done.
 #include "fh_epilogue.h"
 
 namespace fh {
@@ -24,52 +24,52 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
 constexpr int SK_BK = 64;              // K rows a wave's step
 constexpr int SK_LD = SK_BK + 8;       // a column of the wave's bf16 weight tile in LDS
 constexpr int SK_TILE = 32 * SK_LD;    // the wave's tile, bf16 values: 4,608 bytes
-constexpr int SK_MAXW = 16;
 
 
 __device__ inline uint32_t sk_pack_exact(float lo, float hi) {
   return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
 }
 
+// threads a workgroup at most: fewer where a lane holds more (fp32 x, 64 rows), so that registers do not spill
+__host__ __device__ constexpr int skinny_threads(bool xbf16, int mb) { return xbf16 ? (mb == 1 ? 1024 : 512) : (mb == 1 ? 512 : 256); }
+
 template <bool FOUR, bool XBF16, bool NORM, int MB>
-__global__ __launch_bounds__(MB == 1 ? 1024 : 512) void skinny_kernel(MatArgs a, SkinnyMoe moe) {
+__global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatArgs a, SkinnyMoe moe) {
   constexpr int RB = FOUR ? 8 : 16;
+  constexpr int XW = XBF16 ? 1 : 2;  // 16-byte loads for 8 of x's values
   using Half = typename std::conditional<FOUR, uint32_t, uint2>::type;
   extern __shared__ __attribute__((aligned(16))) char sk_smem[];
   __shared__ float rs_s[32 * MB];
   __shared__ float scale_s[32 * MB];
   __shared__ int any_s;
-  __shared__ uint8_t used_s[256];  // stacked experts: whether any row picked expert x
 
   const int item = blockIdx.x, e = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), W = blockDim.x >> 6;
   const int M = (int)a.M, K = (int)a.K;
 
-  // the row scales for this expert; an expert no row picked writes its zeros and reads nothing
+  // the rows' weights for this expert; an expert no row picked writes its zeros and reads nothing
   if (t == 0) any_s = moe.row_scale ? 0 : 1;
   __syncthreads();
   if (t < 32 * MB) {
     float sc = 1.f;
-    if (moe.row_scale && moe.k_expert == 0) sc = t < M ? moe.row_scale[(int64_t)t * moe.experts + e] : 0.f;
+    if (moe.row_scale) {
+      const float r = t < M ? moe.row_scale[(int64_t)t * moe.experts + e] : 0.f;
+      if (r != 0.f) any_s = 1;
+      if (moe.scale_rows) sc = r;
+    }
     scale_s[t] = sc;
-    if (moe.row_scale && moe.k_expert == 0 && sc != 0.f) any_s = 1;
   }
-  if (moe.k_expert > 0 && t < moe.experts) {
-    bool used = !moe.row_scale;
-    for (int m = 0; m < M && !used; ++m) used = moe.row_scale[(int64_t)m * moe.experts + t] != 0.f;
-    used_s[t] = used;
-    if (used) any_s = 1;
-  }
-  // each row's 1 / rms, from the sums of squares its maker left by runs of 16
-  if (t < 32 * MB) {
+  // each row's 1 / rms from the sums of squares its maker left by runs of 16: wave w the rows w, w + W, ..
+  for (int row = wave; row < 32 * MB; row += W) {
     float r = 1.f;
-    if (NORM && t < M) {
-      const float* q = a.ssq_in + (int64_t)t * a.ssq_parts;
+    if (NORM && row < M) {
+      const float* q = a.ssq_in + (int64_t)row * a.ssq_parts;
       float s = 0.f;
-      for (int i = 0; i < a.ssq_parts; ++i) s += q[i];
+      for (int i = lane; i < a.ssq_parts; i += 64) s += q[i];
+      s = wave_sum(s);
       r = 1.0f / sqrtf(s / (float)K + a.eps);
     }
-    rs_s[t] = r;
+    if (lane == 0) rs_s[row] = r;
   }
   __syncthreads();
 
@@ -78,8 +78,8 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void skinny_kernel(MatArgs a,
   if (a.P == 1) { nb[0] = 2 * (int64_t)item; nb[1] = nb[0] + 1; }
   else { nb[0] = pair_first(item, a.pair_half); nb[1] = nb[0] + a.pair_half; }
   const bool run1_ok = nb[1] < a.N / 16;  // (P == 1 with an odd count of runs: the last item's second run is absent)
-  const uint8_t* mant = a.mant + (moe.k_expert ? 0 : (int64_t)e * moe.expert_mant);
-  const uint8_t* exps = a.exps + (moe.k_expert ? 0 : (int64_t)e * moe.expert_exps);
+  const uint8_t* mant = a.mant + (int64_t)e * moe.expert_mant;
+  const uint8_t* exps = a.exps + (int64_t)e * moe.expert_exps;
 
   floatx16 acc[MB];
 #pragma unroll
@@ -88,7 +88,8 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void skinny_kernel(MatArgs a,
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
   uint16_t* Bs = (uint16_t*)sk_smem + wave * SK_TILE;
-  if (any_s) {
+  const int r0 = wave * a.rows, r1 = min(K, r0 + a.rows);
+  if (any_s && r0 < r1) {
     // this lane's weight loads: run lr, rows 4 rq .. 4 rq + 3 of the step, columns 8 ch .. 8 ch + 7
     const int lr = lane >> 5, rq = (lane & 31) >> 1, ch = lane & 1;
     const int64_t run = (lr == 1 && !run1_ok) ? nb[0] : nb[lr];
@@ -96,46 +97,40 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void skinny_kernel(MatArgs a,
     const uint8_t* erun = exps + run * a.K;
     // x's loads: row (lane % 32) of each 32-row block, k 16 s + 8 (lane / 32) .. + 7
     const int xr = lane & 31, xh = lane >> 5;
-    int64_t xrow[MB];
+    const char* xp[MB];
 #pragma unroll
-    for (int b = 0; b < MB; ++b) xrow[b] = min(xr + 32 * b, M - 1);
-    const int r0 = wave * a.rows, r1 = min(K, r0 + a.rows);
-    for (int k0 = r0; k0 < r1; k0 += SK_BK) {
-      if (moe.k_expert > 0 && !used_s[k0 / moe.k_expert]) continue;  // an expert no row picked: nothing to add
-      const int k = min(k0 + 4 * rq, K - 4);
-      Half wm[4];
+    for (int b = 0; b < MB; ++b)
+      xp[b] = (const char*)a.x + ((int64_t)min(xr + 32 * b, M - 1) * a.ldx + (int64_t)e * moe.expert_xcols) * (XBF16 ? 2 : 4);
+    const int last = r1 - SK_BK;  // (r1 - r0 is a multiple of 64: K is)
+
+    // a step's loads (unconditional, a step past the slice re-reads its last: the compiler can count them and wait
+    // for the older set only), two sets in flight
+    auto load = [&](int k0, Half (&wm)[4], uint32_t& we, uint4 (&xv)[MB][4][XW]) {
+      __builtin_amdgcn_sched_barrier(0);  // the loads stay together, in this order, between the steps: a step waits
+                                          // only for its own set, the older one
+      k0 = min(k0, last);
+      const int k = k0 + 4 * rq;
 #pragma unroll
       for (int r = 0; r < 4; ++r) wm[r] = *(const Half*)(mrun + (int64_t)(k + r) * RB);
-      const uint32_t we = *(const uint32_t*)(erun + k);
-      // x: 4 steps of 16 k, 8 values a lane a block (clamped to K; the weight rows past r1 are zero)
-      uint4 xv[MB][4][XBF16 ? 1 : 2];
+      we = *(const uint32_t*)(erun + k);
 #pragma unroll
       for (int b = 0; b < MB; ++b)
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const int kx = min(k0 + 16 * s + 8 * xh, K - 8);
-          const char* p = (const char*)a.x + (xrow[b] * a.ldx + kx) * (XBF16 ? 2 : 4);
-          xv[b][s][0] = *(const uint4*)p;
-          if (!XBF16) xv[b][s][XBF16 ? 0 : 1] = *(const uint4*)(p + 16);
-        }
-      float gw[4][8];
-      if (NORM) {
+          const uint4* p = (const uint4*)(xp[b] + (k0 + 16 * s + 8 * xh) * (XBF16 ? 2 : 4));
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int kx = min(k0 + 16 * s + 8 * xh, K - 8);
-          const float4 g0 = *(const float4*)(a.norm_w + kx), g1 = *(const float4*)(a.norm_w + kx + 4);
-          const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-#pragma unroll
-          for (int i = 0; i < 8; ++i) gw[s][i] = a.centered ? g[i] + 1.f : g[i];
+          for (int i = 0; i < XW; ++i) xv[b][s][i] = p[i];
         }
-      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto step = [&](int k0, bool valid, const Half (&wm)[4], uint32_t we, const uint4 (&xv)[MB][4][XW]) {
       // the weight tile, K-contiguous: 8 columns of 4 rows a lane
       float f[4][8];
 #pragma unroll
       for (int r = 0; r < 4; ++r) magnitudes8(wm[r], f[r]);
       float sc[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = k0 + 4 * rq + r < r1 ? ldexpf(1.f, (int)((we >> (8 * r)) & 255u) - 133) : 0.f;
+      for (int r = 0; r < 4; ++r) sc[r] = valid ? ldexpf(1.f, (int)((we >> (8 * r)) & 255u) - 133) : 0.f;
 #pragma unroll
       for (int c = 0; c < 8; ++c)
         *(uint2*)(Bs + (lr * 16 + ch * 8 + c) * SK_LD + 4 * rq) =
@@ -146,28 +141,51 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void skinny_kernel(MatArgs a,
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const bf16x8 bf = *(const bf16x8*)(Bs + (lane & 31) * SK_LD + 16 * s + 8 * xh);
+        float gw[8];
+        if (NORM) {
+          const int kg = min(k0, last) + 16 * s + 8 * xh;
+          const float4 g0 = *(const float4*)(a.norm_w + kg), g1 = *(const float4*)(a.norm_w + kg + 4);
+          const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) gw[i] = a.centered ? g[i] + 1.f : g[i];
+        }
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
-          float v[8];
-          if (XBF16) {
-            const uint32_t w4[4] = {xv[b][s][0].x, xv[b][s][0].y, xv[b][s][0].z, xv[b][s][0].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { v[2 * j] = __uint_as_float(w4[j] << 16); v[2 * j + 1] = __uint_as_float(w4[j] & 0xFFFF0000u); }
-          } else {
-            const uint4 u0 = xv[b][s][0], u1 = xv[b][s][XBF16 ? 0 : 1];
-            const uint32_t w8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(w8[j]);
-          }
           bf16x8 af;
+          if (XBF16 && !NORM) {
+            af = *(const bf16x8*)&xv[b][s][0];
+          } else {
+            float v[8];
+            if (XBF16) {
+              const uint32_t w4[4] = {xv[b][s][0].x, xv[b][s][0].y, xv[b][s][0].z, xv[b][s][0].w};
 #pragma unroll
-          for (int j = 0; j < 8; ++j) af[j] = (__bf16)(NORM ? v[j] * gw[s][j] : v[j]);
+              for (int j = 0; j < 4; ++j) { v[2 * j] = __uint_as_float(w4[j] << 16); v[2 * j + 1] = __uint_as_float(w4[j] & 0xFFFF0000u); }
+            } else {
+              const uint4 u0 = xv[b][s][0], u1 = xv[b][s][XW - 1];
+              const uint32_t w8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+              for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(w8[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) af[j] = (__bf16)(NORM ? v[j] * gw[j] : v[j]);
+          }
           acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc[b], 0, 0, 0);
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();  // every lane's reads of the tile are done before the next step overwrites it
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    Half w0[4], w1[4];
+    uint32_t e0, e1;
+    uint4 x0[MB][4][XW], x1[MB][4][XW];
+    load(r0, w0, e0, x0);
+    load(r0 + SK_BK, w1, e1, x1);
+    for (int k0 = r0; k0 < r1; k0 += 2 * SK_BK) {  // (an odd count of steps ends with a step of zero weights)
+      step(k0, true, w0, e0, x0);
+      load(k0 + 2 * SK_BK, w0, e0, x0);
+      step(k0 + SK_BK, k0 + SK_BK < r1, w1, e1, x1);
+      load(k0 + 3 * SK_BK, w1, e1, x1);
     }
   }
 
@@ -192,7 +210,7 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void skinny_kernel(MatArgs a,
   __syncthreads();
 
   const int kind = a.kind;
-  const int64_t col_off = moe.k_expert ? 0 : (int64_t)e * moe.expert_cols;
+  const int64_t col_off = (int64_t)e * moe.expert_cols;
   if (a.P == 1) {  // FH_EP_STORE / FH_EP_RESIDUAL: a thread a column of a row; a run is 16 neighbouring lanes
     for (int i = t; i < 32 * MB * 32; i += blockDim.x) {
       const int row = i >> 5, c = i & 31, j = c & 15;
@@ -252,11 +270,11 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void skinny_kernel(MatArgs a,
   }
 }
 
-// W waves: the least power of 2 giving ~4096 waves in all (16 a CU), at most 16 (8 for 64 rows: the sums' tiles fit
-// LDS), each at least one 64-row step
-static void skinny_plan(int64_t K, int items, int experts, int mb, int& W, int& rows) {
+// W waves: the least power of 2 giving ~4096 waves in all (16 a CU), at most what skinny_threads allows (and the
+// sums' tiles fit LDS), each at least one 64-row step
+static void skinny_plan(int64_t K, int items, int experts, int most, int& W, int& rows) {
   int64_t w = 1;
-  while (w < SK_MAXW / mb && w * items * experts < 4096) w *= 2;
+  while (w < most && w * items * experts < 4096) w *= 2;
   const int64_t steps = (K + SK_BK - 1) / SK_BK;
   while (w > 1 && w > steps) w /= 2;
   int64_t r = (K + w - 1) / w;
@@ -281,7 +299,7 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
   const int items = (int)(a0.P == 1 ? (a0.N / 16 + 1) / 2 : a0.items);
   if (experts > 256) return fail(FH_EUNSUP, "skinny matmul: at most 256 experts");
   int W, rows;
-  skinny_plan(a0.K, items, experts, a0.M > 32 ? 2 : 1, W, rows);
+  skinny_plan(a0.K, items, experts, skinny_threads(a0.x_bf16, a0.M > 32 ? 2 : 1) / 64, W, rows);
   for (int64_t m0 = 0; m0 < a0.M; m0 += 64) {
     MatArgs a = a0;
     a.M = a0.M - m0 < 64 ? a0.M - m0 : 64;

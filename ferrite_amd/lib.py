@@ -41,7 +41,7 @@ SIGNATURES = {
   "fh_attention_prefill": ([P, L, P, I, L, I, I, I, I, L, L, P, I, L, P], I),
   "fh_rms_rows": ([P, L, L, L, P, ctypes.c_float, I, P, I, L, P], I),
   "fh_moe_route": ([P, L, I, L, P, ctypes.c_float, I, P, I, I, I, I, P, P, P, P], I),
-  "fh_moe_workspace_bytes": ([I, I, L], S),
+  "fh_moe_workspace_bytes": ([I, I, L, L], S),
   "fh_moe_experts": ([P, L, I, L, P, P, ctypes.c_float, I, I, L, P, P, I, P, P, I, P, P, P, P, P, S, P], I),
   "fh_argmax_rows": ([P, L, L, P, P], I),
   "fh_argmax_parts": ([P, L, L, P, P], I),

@@ -81,11 +81,23 @@ class Decoder:
   fuse leaves them: layers.{l}.input_layernorm, .post_attention_layernorm, .qkv_proj, .o_proj, .gate_up_proj,
   .down_proj (x @ w), norm, embed, embed.T (the output layer; the embedding's transpose when tied)."""
 
-  def __init__(self, c, weights, mode="bfp8", kv="bf16", batch=1, context=256, device="cuda", slots=1):
+  def __init__(self, c, weights, mode="bfp8", kv="bf16", batch=1, context=256, device="cuda", slots=1, mfma_from=9,
+               share=None):
+    """mfma_from: the batch from which a step's matmuls run on the matrix cores (fh_gemm_bfp, bf16 rows) rather than
+    the exact-product GEMV (None: never). share: another Decoder of the same model whose weights this one uses."""
     self.c, self.mode, self.batch, self.context, self.device = c, mode, batch, context, torch.device(device)
     self.prec = precision(c, mode)
     hd = head(c)
     self.hd, self.qkv_cols = hd, (c.heads + 2 * c.kv) * hd
+    self.mm = ops.gemm if mfma_from is not None and batch >= mfma_from else ops.gemv
+    if share is not None:
+      self.layers, self.norm, self.embed, self.head, self.cos, self.sin = share.layers, share.norm, share.embed, share.head, share.cos, share.sin
+    else:
+      self._load(weights)
+    self._buffers(kv, batch, context, slots)
+
+  def _load(self, weights):
+    c, hd = self.c, self.hd
     f32 = lambda t: t.to(self.device, torch.float32).contiguous()
     gpu = lambda t: t.to(self.device)
     self.layers = []
@@ -106,6 +118,9 @@ class Decoder:
     self.head = ops.pack(head_w.contiguous(), self.prec["head", None])
     cos, sin = rotary_tables(c, c.places)
     self.cos, self.sin = torch.from_numpy(cos).to(self.device), torch.from_numpy(sin).to(self.device)
+
+  def _buffers(self, kv, batch, context, slots):
+    c, hd = self.c, self.hd
     # the KV cache: a block's keys' heads then values', `slots` sequences' rows side by side (models/llama.py:506-514)
     self.slots = slots or 1
     self.part = context  # rows a sequence
@@ -149,16 +164,16 @@ class Decoder:
                         heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
                         places=self.places, cache_rows=self.rows, cache=self.cache[l],
                         cache_dtype=lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"], cache_len=self.cache[l].shape[1])
-      ops.gemv(self.x, L.qkv, ep, out=self.q)
+      self.mm(self.x, L.qkv, ep, out=self.q)
       ops.attention_decode(self.q, self.cache[l], c.heads, c.kv, hd, self.places, self.first, self.context, self.ws, o=self.att)
       ep = ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq)
-      ops.gemv(self.att, L.o, ep, out=self.x)
+      self.mm(self.att, L.o, ep, out=self.x)
       ep = ops.epilogue(lib.EP_SILU_GATE, norm_w=L.norm2, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered), split=c.ffn)
-      ops.gemv(self.x, L.gate_up, ep, out=self.h)
+      self.mm(self.x, L.gate_up, ep, out=self.h)
       ep = ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq)
-      ops.gemv(self.h, L.down, ep, out=self.x)
+      self.mm(self.h, L.down, ep, out=self.x)
     ep = ops.epilogue(lib.EP_STORE, norm_w=self.norm, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered), argmax_parts=self.parts)
-    ops.gemv(self.x, self.head, ep, out=self.logits)
+    self.mm(self.x, self.head, ep, out=self.logits)
     ops.argmax_parts(self.parts, self.picks)
 
   def _prefill_buffers(self, T):

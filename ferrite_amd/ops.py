@@ -161,7 +161,7 @@ def moe_route(x, router, experts, k, norm_topk=True, norm_w=None, eps=1e-5, cent
 @dataclass
 class Experts:
   """A mixture of experts' weights on the GPU: gate_up, the experts' [dim][2 ffn] packed one after another; down, the
-  experts' [ffn][dim] stacked into one [experts * ffn][dim] matrix, packed."""
+  experts' [ffn][dim] packed one after another."""
   gate_up: BfpWeight
   down: BfpWeight
   experts: int
@@ -175,7 +175,8 @@ def pack_experts(gate_up, down, fmt="bfp4"):
   ffn = two // 2
   parts = [pack(gate_up[e], fmt) for e in range(E)]
   gu = BfpWeight(torch.cat([p.mant for p in parts]), torch.cat([p.exps for p in parts]), dim, 2 * ffn, fmt)
-  dn = pack(down.reshape(E * ffn, dim), fmt)
+  parts = [pack(down[e], fmt) for e in range(E)]
+  dn = BfpWeight(torch.cat([p.mant for p in parts]), torch.cat([p.exps for p in parts]), ffn, dim, fmt)
   return Experts(gu, dn, E, dim, ffn)
 
 
@@ -184,7 +185,7 @@ def moe_experts(x, ex, dense, out=None, residual=None, ssq_out=None, norm_w=None
   _dev(x, dense, out, residual, ssq_out, norm_w, ssq_in)
   rows = x.shape[0]
   if out is None: out = torch.empty(rows, ex.dim, dtype=torch.float32, device=x.device)
-  n = lib.load().fh_moe_workspace_bytes(rows, ex.experts, ex.ffn)
+  n = lib.load().fh_moe_workspace_bytes(rows, ex.experts, ex.ffn, ex.dim)
   if ws is None or ws.numel() < n: ws = torch.empty(max(n, 256), dtype=torch.uint8, device=x.device)
   lib.call("fh_moe_experts", _ptr(x), x.stride(0), rows, ex.dim, _ptr(norm_w), _ptr(ssq_in), eps, int(centered),
            ex.experts, ex.ffn, _ptr(ex.gate_up.mant), _ptr(ex.gate_up.exps), lib.DTYPES[ex.gate_up.fmt], _ptr(ex.down.mant),

@@ -175,10 +175,11 @@ int fh_moe_route(const float* x, int64_t ldx, int rows, int64_t dim, const float
 /* The chosen experts' SwiGLUs, weighted and summed (numpy_experts / chip_experts' dense path, models/llama.py:294-321):
  * y = residual + sum_e dense[:, e] * (silu(h @ gate_e) * (h @ up_e)) @ down_e, h = x with the RMSNorm prologue
  * (norm_w, ssq_in as fh_gemv_bfp's). gate_up: the experts' [dim][2 ffn] weights packed one after another (FH_AXIS_N);
- * down: the experts' [ffn][dim] weights stacked into one [experts * ffn][dim] matrix, packed. An expert no row picked
- * reads no weight. residual NULL: y is the sum alone; ssq_out: y's sums of squares by 16 columns. On the matrix
- * cores, x in bf16 (fh_gemm_bfp's arithmetic). Workspace: fh_moe_workspace_bytes (the gate_up outputs of 64 rows). */
-size_t fh_moe_workspace_bytes(int rows, int experts, int64_t ffn);
+ * down: the experts' [ffn][dim] weights packed one after another. An expert no row picked reads no weight. residual
+ * NULL: y is the sum alone; ssq_out: y's sums of squares by 16 columns. On the matrix cores, x and the SwiGLU outputs
+ * in bf16 (fh_gemm_bfp's arithmetic); the experts' outputs summed in expert order. dim and ffn multiples of 64.
+ * Workspace: fh_moe_workspace_bytes (a pass of 64 rows' gate_up and down outputs). */
+size_t fh_moe_workspace_bytes(int rows, int experts, int64_t ffn, int64_t dim);
 int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim, const float* norm_w, const float* ssq_in, float eps,
                    int centered, int experts, int64_t ffn, const void* gu_mant, const uint8_t* gu_exps, int gu_fmt,
                    const void* down_mant, const uint8_t* down_exps, int down_fmt, const float* dense, float* y,

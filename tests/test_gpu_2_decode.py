@@ -11,10 +11,11 @@ from oracle import llama as OL
 pytestmark = pytest.mark.gpu
 
 
-def decoder(c, w, mode, kv, batch=1, context=256):
+def decoder(c, w, mode, kv, batch=1, context=256, mfma_from=None):
+  # (mfma_from None: every row through the exact-product GEMV, whose logits are within fp32 summation of numpy's)
   from ferrite_amd import llama as G
   gc = G.model(**{k: getattr(c, k) for k in ("dim", "heads", "kv", "layers", "eps", "theta", "vocab", "ffn", "places", "rope", "tied")})
-  return G.Decoder(gc, G.numpy_weights(w), mode=mode, kv=kv, batch=batch, context=context)
+  return G.Decoder(gc, G.numpy_weights(w), mode=mode, kv=kv, batch=batch, context=context, mfma_from=mfma_from)
 
 
 def greedy(c, w, mode, kv, prompt, steps, context):
@@ -50,6 +51,31 @@ def greedy(c, w, mode, kv, prompt, steps, context):
     one.advance()
     one.step()
   return want, got, want_logits, got_logits
+
+
+def test_batch16_decode_on_matrix_cores(cuda):
+  # 16 sequences a step (benchmark config 3's batch 16) take the skinny matrix-core kernel (bf16 rows): each row's
+  # logits within the north star's bar of numpy's, 4 steps of each sequence at its own slot of the cache
+  rng = np.random.default_rng(15)
+  c = smol(2, 512)
+  w = OL.random_weights(c, rng)
+  prec = OL.precision(c, "bfp8", "bf16")
+  c.precision, c.kv_rounded = prec, True
+  arrays = OL.arrays(w, prec)
+  B, ctx = 16, 32
+  from ferrite_amd import llama as G
+  weights = decoder(c, w, "bfp8", "bf16", context=ctx)
+  dec = G.Decoder(weights.c, None, mode="bfp8", kv="bf16", batch=B, context=ctx, slots=B, mfma_from=9, share=weights)
+  assert dec.mm.__name__ == "gemm"
+  toks = rng.integers(0, 512, (B, 4))
+  caches = [OL.kv_cache(c, ctx) for _ in range(B)]
+  for p in range(4):
+    logits = dec.step(toks[:, p].tolist(), [p] * B, slots=list(range(B)), replay=False)[0].cpu().numpy()
+    for b in range(B):
+      want = OL.forward([int(toks[b, p])], [p], arrays, c, caches[b])[0]
+      rel = np.abs(logits[b] - want).max() / np.abs(want).max()
+      cos = (logits[b] * want).sum() / np.linalg.norm(logits[b]) / np.linalg.norm(want)
+      assert rel <= 1e-2 and cos >= 0.9999, (p, b, rel, cos)
 
 
 def smol(layers, vocab, places=256):
