@@ -3,44 +3,48 @@
 // RMSNorm weight rounded to bf16, the weight's values exact, fp32 sums).
 //
 // Built like the decode GEMV: a workgroup takes one item of 32 columns (two runs of 16, or a RoPE / SiLU·gate pair)
-// and its W waves split K; nothing crosses workgroups. A wave walks its K slice 64 rows at a time: each lane loads 4
-// rows x 8 columns of the weight (the same 1 KiB of a run's rows a wave as the GEMV), turns them into bf16 and writes
-// them K-contiguous into the wave's own LDS (no workgroup barrier in the loop: a wave reads back only what it wrote),
-// loads x's rows for the same 64 k, and issues v_mfma_f32_32x32x16_bf16: 32 rows x 32 columns x 16 k each. The waves'
-// 32 x 32 (or 64 x 32) sums then meet in LDS in a fixed order and the epilogue runs on the item's outputs.
+// and its W waves split K; nothing crosses workgroups. A wave walks its K slice 64 rows at a time and reads the
+// weight as the GEMV does: a lane a row of a run (16 bytes of bfp8, 8 of bfp4, and its exponent byte), a wave's loads
+// 1 KiB (512 B) contiguous, four steps of them in flight. A lane turns its row into 16 bf16 values and writes them
+// row-major into the wave's own LDS tile (no workgroup barrier in the loop: a wave reads back only what it wrote);
+// ds_read_b64_tr_b16 then reads the tile back K-contiguous, as v_mfma_f32_16x16x32_bf16 takes its operand (in each
+// 16-lane group, lane 4m + q addresses row m, columns 4q .. 4q + 3; lane j receives column j of the four rows). x's
+// rows (16 a block, up to 4 blocks) come straight from memory, 8 consecutive k a lane, a step ahead. The waves' sums
+// then meet in LDS in a fixed order and the epilogue runs on the item's outputs.
 //
 // For a mixture of experts the grid's second dimension is the expert: the weight is the expert's (`expert_mant` /
-// `expert_exps` bytes apart), its outputs go `expert_cols` columns further on, and (scale_rows) each row's output is
-// scaled by that row's weight for the expert (0 where the row did not pick it); an expert no row picked reads nothing.
-//
-// A wave keeps two steps' loads in flight: each step's loads go out right after the step two before it is done.
+// `expert_exps` bytes apart), its outputs go `expert_cols` columns further on (and its x `expert_xcols`), and
+// (scale_rows) each row's output is scaled by that row's weight for the expert (0 where the row did not pick it); an
+// expert no row picked reads nothing.
 #include "fh_epilogue.h"
 
 namespace fh {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short short4v;
+#define FH_LDS __attribute__((address_space(3)))
 
-constexpr int SK_BK = 64;              // K rows a wave's step
-constexpr int SK_LD = SK_BK + 8;       // a column of the wave's bf16 weight tile in LDS
-constexpr int SK_TILE = 32 * SK_LD;    // the wave's tile, bf16 values: 4,608 bytes
-
+constexpr int SK_BK = 64;              // K rows a wave's step (a lane a row)
+constexpr int SK_RS = 40;              // a row of the wave's bf16 tile in LDS: 32 columns + 8 (80 bytes: banks spread)
+constexpr int SK_TILE = SK_BK * SK_RS; // the wave's tile, bf16 values: 5,120 bytes
+constexpr int SK_RING = 4;             // steps of weight loads in flight
 
 __device__ inline uint32_t sk_pack_exact(float lo, float hi) {
   return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
 }
 
-// threads a workgroup at most: fewer where a lane holds more (fp32 x, 64 rows), so that registers do not spill
-__host__ __device__ constexpr int skinny_threads(bool xbf16, int mb) { return xbf16 ? (mb == 1 ? 1024 : 512) : (mb == 1 ? 512 : 256); }
+// threads a workgroup at most: fewer where a lane holds more, so that registers do not spill
+__host__ __device__ constexpr int skinny_threads(bool xbf16, int mb) { return (xbf16 && mb == 1) ? 1024 : 512; }
 
-template <bool FOUR, bool XBF16, bool NORM, int MB>
+template <bool FOUR, bool XBF16, bool NORM, int MB>  // MB: blocks of 16 rows
 __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatArgs a, SkinnyMoe moe) {
   constexpr int RB = FOUR ? 8 : 16;
-  constexpr int XW = XBF16 ? 1 : 2;  // 16-byte loads for 8 of x's values
-  using Half = typename std::conditional<FOUR, uint32_t, uint2>::type;
+  constexpr int XW = XBF16 ? 1 : 2;    // 16-byte loads for 8 of x's values
+  using Row = typename std::conditional<FOUR, uint2, uint4>::type;
   extern __shared__ __attribute__((aligned(16))) char sk_smem[];
-  __shared__ float rs_s[32 * MB];
-  __shared__ float scale_s[32 * MB];
+  __shared__ float rs_s[16 * MB];
+  __shared__ float scale_s[16 * MB];
   __shared__ int any_s;
 
   const int item = blockIdx.x, e = blockIdx.y;
@@ -50,7 +54,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   // the rows' weights for this expert; an expert no row picked writes its zeros and reads nothing
   if (t == 0) any_s = moe.row_scale ? 0 : 1;
   __syncthreads();
-  if (t < 32 * MB) {
+  if (t < 16 * MB) {
     float sc = 1.f;
     if (moe.row_scale) {
       const float r = t < M ? moe.row_scale[(int64_t)t * moe.experts + e] : 0.f;
@@ -60,7 +64,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
     scale_s[t] = sc;
   }
   // each row's 1 / rms from the sums of squares its maker left by runs of 16: wave w the rows w, w + W, ..
-  for (int row = wave; row < 32 * MB; row += W) {
+  for (int row = wave; row < 16 * MB; row += W) {
     float r = 1.f;
     if (NORM && row < M) {
       const float* q = a.ssq_in + (int64_t)row * a.ssq_parts;
@@ -81,87 +85,105 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   const uint8_t* mant = a.mant + (int64_t)e * moe.expert_mant;
   const uint8_t* exps = a.exps + (int64_t)e * moe.expert_exps;
 
-  floatx16 acc[MB];
+  floatx4 acc[MB][2];  // [16-row block][run]: lane l holds rows 4 (l / 16) + i, column l % 16 of the run
 #pragma unroll
-  for (int i = 0; i < MB; ++i)
+  for (int b = 0; b < MB; ++b)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+    for (int j = 0; j < 2; ++j) acc[b][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   uint16_t* Bs = (uint16_t*)sk_smem + wave * SK_TILE;
   const int r0 = wave * a.rows, r1 = min(K, r0 + a.rows);
   if (any_s && r0 < r1) {
-    // this lane's weight loads: run lr, rows 4 rq .. 4 rq + 3 of the step, columns 8 ch .. 8 ch + 7
-    const int lr = lane >> 5, rq = (lane & 31) >> 1, ch = lane & 1;
-    const int64_t run = (lr == 1 && !run1_ok) ? nb[0] : nb[lr];
-    const uint8_t* mrun = mant + run * a.K * RB + ch * (RB / 2);
-    const uint8_t* erun = exps + run * a.K;
-    // x's loads: row (lane % 32) of each 32-row block, k 16 s + 8 (lane / 32) .. + 7
-    const int xr = lane & 31, xh = lane >> 5;
+    const uint8_t* mrun[2];
+    const uint8_t* erun[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t run = (j == 1 && !run1_ok) ? nb[0] : nb[j];
+      mrun[j] = mant + run * a.K * RB;
+      erun[j] = exps + run * a.K;
+    }
+    // x: row 16 b + lane % 16, k 8 (lane / 16) .. + 7 of each 32 k
     const char* xp[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b)
-      xp[b] = (const char*)a.x + ((int64_t)min(xr + 32 * b, M - 1) * a.ldx + (int64_t)e * moe.expert_xcols) * (XBF16 ? 2 : 4);
+      xp[b] = (const char*)a.x + ((int64_t)min(16 * b + (lane & 15), M - 1) * a.ldx + (int64_t)e * moe.expert_xcols + 8 * (lane >> 4)) * (XBF16 ? 2 : 4);
     const int last = r1 - SK_BK;  // (r1 - r0 is a multiple of 64: K is)
+    // the transposed reads' addresses in the tile: 16-lane group g reads k 8 (g / 2)... of the 32-k block; in the
+    // group, lane 4 m + q points at row m, columns 4 q .. 4 q + 3 of the run
+    const int g = lane >> 4, m4 = (lane & 15) >> 2, q4 = lane & 3;
+    FH_LDS short4v* trp = (FH_LDS short4v*)(Bs + (8 * g + m4) * SK_RS + 4 * q4);
 
-    // a step's loads (unconditional, a step past the slice re-reads its last: the compiler can count them and wait
-    // for the older set only), two sets in flight
-    auto load = [&](int k0, Half (&wm)[4], uint32_t& we, uint4 (&xv)[MB][4][XW]) {
-      __builtin_amdgcn_sched_barrier(0);  // the loads stay together, in this order, between the steps: a step waits
-                                          // only for its own set, the older one
-      k0 = min(k0, last);
-      const int k = k0 + 4 * rq;
+    Row wr[SK_RING][2];
+    uint32_t we[SK_RING][2];
+    auto load_w = [&](int k0, Row (&w)[2], uint32_t (&ex)[2]) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int k = min(k0, last) + lane;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) wm[r] = *(const Half*)(mrun + (int64_t)(k + r) * RB);
-      we = *(const uint32_t*)(erun + k);
+      for (int j = 0; j < 2; ++j) { w[j] = *(const Row*)(mrun[j] + (int64_t)k * RB); ex[j] = erun[j][k]; }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    uint4 xv[2][MB][2][XW];  // [set][block][k32 half][16 bytes]
+    auto load_x = [&](int k0, uint4 (&xs)[MB][2][XW]) {
+      __builtin_amdgcn_sched_barrier(0);
+      k0 = min(k0, last);
 #pragma unroll
       for (int b = 0; b < MB; ++b)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const uint4* p = (const uint4*)(xp[b] + (k0 + 16 * s + 8 * xh) * (XBF16 ? 2 : 4));
+        for (int h = 0; h < 2; ++h) {
+          const uint4* p = (const uint4*)(xp[b] + (int64_t)(k0 + 32 * h) * (XBF16 ? 2 : 4));
 #pragma unroll
-          for (int i = 0; i < XW; ++i) xv[b][s][i] = p[i];
+          for (int i = 0; i < XW; ++i) xs[b][h][i] = p[i];
         }
       __builtin_amdgcn_sched_barrier(0);
     };
-    auto step = [&](int k0, bool valid, const Half (&wm)[4], uint32_t we, const uint4 (&xv)[MB][4][XW]) {
-      // the weight tile, K-contiguous: 8 columns of 4 rows a lane
-      float f[4][8];
+    auto step = [&](int k0, bool valid, const Row (&w)[2], const uint32_t (&ex)[2], const uint4 (&xs)[MB][2][XW]) {
+      // the lane's two rows -> 16 bf16 values each, row-major into the tile (rows past the slice: zero)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) magnitudes8(wm[r], f[r]);
-      float sc[4];
+      for (int j = 0; j < 2; ++j) {
+        float f[16];
+        magnitudes(w[j], f);
+        const float sc = valid ? ldexpf(1.f, (int)ex[j] - 133) : 0.f;
+        uint32_t p[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = valid ? ldexpf(1.f, (int)((we >> (8 * r)) & 255u) - 133) : 0.f;
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-        *(uint2*)(Bs + (lr * 16 + ch * 8 + c) * SK_LD + 4 * rq) =
-            make_uint2(sk_pack_exact(f[0][c] * sc[0], f[1][c] * sc[1]), sk_pack_exact(f[2][c] * sc[2], f[3][c] * sc[3]));
+        for (int i = 0; i < 8; ++i) p[i] = sk_pack_exact(f[2 * i] * sc, f[2 * i + 1] * sc);
+        uint4* dst = (uint4*)(Bs + lane * SK_RS + 16 * j);
+        dst[0] = make_uint4(p[0], p[1], p[2], p[3]);
+        dst[1] = make_uint4(p[4], p[5], p[6], p[7]);
+      }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 bf = *(const bf16x8*)(Bs + (lane & 31) * SK_LD + 16 * s + 8 * xh);
+      for (int h = 0; h < 2; ++h) {  // the step's two blocks of 32 k
+        bf16x8 bfr[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(trp + (32 * h * SK_RS + 16 * j) / 4);
+          const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(trp + (32 * h * SK_RS + 4 * SK_RS + 16 * j) / 4);
+          const short v8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          bfr[j] = *(const bf16x8*)v8;
+        }
         float gw[8];
         if (NORM) {
-          const int kg = min(k0, last) + 16 * s + 8 * xh;
+          const int kg = min(k0, last) + 32 * h + 8 * (lane >> 4);
           const float4 g0 = *(const float4*)(a.norm_w + kg), g1 = *(const float4*)(a.norm_w + kg + 4);
-          const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+          const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
 #pragma unroll
-          for (int i = 0; i < 8; ++i) gw[i] = a.centered ? g[i] + 1.f : g[i];
+          for (int i = 0; i < 8; ++i) gw[i] = a.centered ? gg[i] + 1.f : gg[i];
         }
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
           bf16x8 af;
           if (XBF16 && !NORM) {
-            af = *(const bf16x8*)&xv[b][s][0];
+            af = *(const bf16x8*)&xs[b][h][0];
           } else {
             float v[8];
             if (XBF16) {
-              const uint32_t w4[4] = {xv[b][s][0].x, xv[b][s][0].y, xv[b][s][0].z, xv[b][s][0].w};
+              const uint32_t w4[4] = {xs[b][h][0].x, xs[b][h][0].y, xs[b][h][0].z, xs[b][h][0].w};
 #pragma unroll
               for (int j = 0; j < 4; ++j) { v[2 * j] = __uint_as_float(w4[j] << 16); v[2 * j + 1] = __uint_as_float(w4[j] & 0xFFFF0000u); }
             } else {
-              const uint4 u0 = xv[b][s][0], u1 = xv[b][s][XW - 1];
+              const uint4 u0 = xs[b][h][0], u1 = xs[b][h][XW - 1];
               const uint32_t w8[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
               for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(w8[j]);
@@ -169,42 +191,46 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
 #pragma unroll
             for (int j = 0; j < 8; ++j) af[j] = (__bf16)(NORM ? v[j] * gw[j] : v[j]);
           }
-          acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc[b], 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[b][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[j], acc[b][j], 0, 0, 0);
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();  // every lane's reads of the tile are done before the next step overwrites it
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
-    Half w0[4], w1[4];
-    uint32_t e0, e1;
-    uint4 x0[MB][4][XW], x1[MB][4][XW];
-    load(r0, w0, e0, x0);
-    load(r0 + SK_BK, w1, e1, x1);
-    for (int k0 = r0; k0 < r1; k0 += 2 * SK_BK) {  // (an odd count of steps ends with a step of zero weights)
-      step(k0, true, w0, e0, x0);
-      load(k0 + 2 * SK_BK, w0, e0, x0);
-      step(k0 + SK_BK, k0 + SK_BK < r1, w1, e1, x1);
-      load(k0 + 3 * SK_BK, w1, e1, x1);
+#pragma unroll
+    for (int i = 0; i < SK_RING; ++i) load_w(r0 + SK_BK * i, wr[i], we[i]);
+    load_x(r0, xv[0]);
+    for (int k0 = r0; k0 < r1; k0 += SK_RING * SK_BK) {  // (steps past the slice carry zero weights)
+#pragma unroll
+      for (int i = 0; i < SK_RING; ++i) {
+        const int k = k0 + SK_BK * i;
+        load_x(k + SK_BK, xv[(i + 1) & 1]);
+        step(k, k < r1, wr[i], we[i], xv[i & 1]);
+        load_w(k + SK_RING * SK_BK, wr[i], we[i]);
+      }
     }
   }
 
-  // the waves' sums meet in LDS, in wave order: block b's value r of lane l is row 32 b + 8 (r / 4) + 4 (l / 32) +
-  // r % 4, column l % 32
+  // the waves' sums meet in LDS, in wave order: block b, run j's value i of lane l is row 16 b + 4 (l / 16) + i,
+  // column 16 j + l % 16
   __syncthreads();
-  float* part = (float*)sk_smem;  // [W][32 MB][33]
+  float* part = (float*)sk_smem;  // [W][16 MB][33]
   constexpr int PLD = 33;
 #pragma unroll
   for (int b = 0; b < MB; ++b)
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      part[(wave * 32 * MB + 32 * b + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * PLD + (lane & 31)] = acc[b][r];
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        part[(wave * 16 * MB + 16 * b + 4 * (lane >> 4) + i) * PLD + 16 * j + (lane & 15)] = acc[b][j][i];
   __syncthreads();
-  float* fin = part + W * 32 * MB * PLD;  // [32 MB][33]
-  for (int i = t; i < 32 * MB * 32; i += blockDim.x) {
+  float* fin = part + W * 16 * MB * PLD;  // [16 MB][33]
+  for (int i = t; i < 16 * MB * 32; i += blockDim.x) {
     const int row = i >> 5, col = i & 31;
     float s = 0.f;
-    for (int w = 0; w < W; ++w) s += part[(w * 32 * MB + row) * PLD + col];
+    for (int w = 0; w < W; ++w) s += part[(w * 16 * MB + row) * PLD + col];
     fin[row * PLD + col] = s * rs_s[row];
   }
   __syncthreads();
@@ -212,7 +238,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   const int kind = a.kind;
   const int64_t col_off = (int64_t)e * moe.expert_cols;
   if (a.P == 1) {  // FH_EP_STORE / FH_EP_RESIDUAL: a thread a column of a row; a run is 16 neighbouring lanes
-    for (int i = t; i < 32 * MB * 32; i += blockDim.x) {
+    for (int i = t; i < 16 * MB * 32; i += blockDim.x) {
       const int row = i >> 5, c = i & 31, j = c & 15;
       const int64_t run = nb[c >> 4];
       const bool ok = row < M && (c < 16 || run1_ok);
@@ -239,7 +265,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       }
     }
   } else {  // the pair: columns 0..15 the first run (gate, or a head's first half), 16..31 its partner
-    for (int i = t; i < 32 * MB * 16; i += blockDim.x) {
+    for (int i = t; i < 16 * MB * 16; i += blockDim.x) {
       const int row = i >> 4, j = i & 15;
       if (row >= M) continue;
       float x0 = fin[row * PLD + j], x1 = fin[row * PLD + 16 + j];
@@ -286,11 +312,12 @@ static void skinny_plan(int64_t K, int items, int experts, int most, int& W, int
 template <bool FOUR, bool XBF16, bool NORM>
 static void skinny_launch(const MatArgs& a, const SkinnyMoe& moe, int items, int experts, int W, int mb, hipStream_t s) {
   const dim3 g(items, experts), b(64 * W);
-  const size_t lds = (size_t)W * 32 * mb * 33 * 4 + 32 * mb * 33 * 4;  // the sums' tiles (they reuse the weight tiles)
+  const size_t lds = (size_t)(W + 1) * 16 * mb * 33 * 4;  // the sums' tiles (they reuse the weight tiles)
   const size_t tiles = (size_t)W * SK_TILE * 2;
   const size_t bytes = lds > tiles ? lds : tiles;
   if (mb == 1) hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 1>), g, b, bytes, s, a, moe);
-  else hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 2>), g, b, bytes, s, a, moe);
+  else if (mb == 2) hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 2>), g, b, bytes, s, a, moe);
+  else hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 4>), g, b, bytes, s, a, moe);
 }
 
 // M rows (at most 64 a pass) of a [grouped] skinny matmul; the caller checked the epilogue
@@ -299,7 +326,8 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
   const int items = (int)(a0.P == 1 ? (a0.N / 16 + 1) / 2 : a0.items);
   if (experts > 256) return fail(FH_EUNSUP, "skinny matmul: at most 256 experts");
   int W, rows;
-  skinny_plan(a0.K, items, experts, skinny_threads(a0.x_bf16, a0.M > 32 ? 2 : 1) / 64, W, rows);
+  const int mb0 = a0.M > 32 ? 4 : a0.M > 16 ? 2 : 1;
+  skinny_plan(a0.K, items, experts, skinny_threads(a0.x_bf16, mb0) / 64, W, rows);
   for (int64_t m0 = 0; m0 < a0.M; m0 += 64) {
     MatArgs a = a0;
     a.M = a0.M - m0 < 64 ? a0.M - m0 : 64;
@@ -313,7 +341,7 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
     if (a.argmax_parts) a.argmax_parts += m0 * (a0.N / 16);
     SkinnyMoe mo = moe;
     if (mo.row_scale) mo.row_scale += m0 * mo.experts;
-    const int mb = a.M > 32 ? 2 : 1;
+    const int mb = a.M > 32 ? 4 : a.M > 16 ? 2 : 1;
     const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
     switch (which) {
       case 0: skinny_launch<false, false, false>(a, mo, items, experts, W, mb, s); break;
