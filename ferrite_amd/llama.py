@@ -136,6 +136,8 @@ class Decoder:
     self.x, self.ssq = z(B, c.dim), z(B, c.dim // 16)
     self.q, self.att = z(B, c.heads * hd), z(B, c.heads * hd)
     self.h = z(B, c.ffn)
+    self.xn = torch.zeros(B, c.dim, dtype=torch.bfloat16, device=self.device)   # the matrix cores' normed rows
+    self.hb = torch.zeros(B, c.ffn, dtype=torch.bfloat16, device=self.device)
     self.logits = z(B, c.vocab)
     self.picks = torch.zeros(B, dtype=torch.int32, device=self.device)
     self.parts = torch.zeros(B, c.vocab // 16, dtype=torch.int64, device=self.device)  # each run of 16 logits' best
@@ -157,6 +159,7 @@ class Decoder:
     self.rows.copy_(slots * self.part + places)
 
   def _step(self):
+    if self.mm is ops.gemm: return self._step_rows()
     c, B, hd = self.c, self.batch, self.hd
     ops.embed_rows(self.embed, self.ids, self.x, self.ssq)
     for l, L in enumerate(self.layers):
@@ -164,16 +167,37 @@ class Decoder:
                         heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
                         places=self.places, cache_rows=self.rows, cache=self.cache[l],
                         cache_dtype=lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"], cache_len=self.cache[l].shape[1])
-      self.mm(self.x, L.qkv, ep, out=self.q)
+      ops.gemv(self.x, L.qkv, ep, out=self.q)
       ops.attention_decode(self.q, self.cache[l], c.heads, c.kv, hd, self.places, self.first, self.context, self.ws, o=self.att)
       ep = ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq)
-      self.mm(self.att, L.o, ep, out=self.x)
+      ops.gemv(self.att, L.o, ep, out=self.x)
       ep = ops.epilogue(lib.EP_SILU_GATE, norm_w=L.norm2, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered), split=c.ffn)
-      self.mm(self.x, L.gate_up, ep, out=self.h)
+      ops.gemv(self.x, L.gate_up, ep, out=self.h)
       ep = ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq)
-      self.mm(self.h, L.down, ep, out=self.x)
+      ops.gemv(self.h, L.down, ep, out=self.x)
     ep = ops.epilogue(lib.EP_STORE, norm_w=self.norm, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered), argmax_parts=self.parts)
-    self.mm(self.x, self.head, ep, out=self.logits)
+    ops.gemv(self.x, self.head, ep, out=self.logits)
+    ops.argmax_parts(self.parts, self.picks)
+
+  def _step_rows(self):
+    """A step of many rows on the matrix cores: each RMSNorm its own kernel writing bf16 rows (the skinny kernel's
+    fast input), SwiGLU's output bf16, the residual stream fp32."""
+    c, B, hd = self.c, self.batch, self.hd
+    ops.embed_rows(self.embed, self.ids, self.x, self.ssq)
+    cache_dtype = lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"]
+    for l, L in enumerate(self.layers):
+      ops.rms_rows(self.x, L.norm1, c.eps, c.centered, out=self.xn)
+      ep = ops.epilogue(lib.EP_ROPE_KV, heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
+                        places=self.places, cache_rows=self.rows, cache=self.cache[l], cache_dtype=cache_dtype,
+                        cache_len=self.cache[l].shape[1])
+      ops.gemm(self.xn, L.qkv, ep, out=self.q)
+      ops.attention_decode(self.q, self.cache[l], c.heads, c.kv, hd, self.places, self.first, self.context, self.ws, o=self.att)
+      ops.gemm(self.att, L.o, ops.epilogue(lib.EP_RESIDUAL, residual=self.x), out=self.x)
+      ops.rms_rows(self.x, L.norm2, c.eps, c.centered, out=self.xn)
+      ops.gemm(self.xn, L.gate_up, ops.epilogue(lib.EP_SILU_GATE, split=c.ffn), out=self.hb)
+      ops.gemm(self.hb, L.down, ops.epilogue(lib.EP_RESIDUAL, residual=self.x), out=self.x)
+    ops.rms_rows(self.x, self.norm, c.eps, c.centered, out=self.xn)
+    ops.gemm(self.xn, self.head, ops.epilogue(lib.EP_STORE, argmax_parts=self.parts), out=self.logits)
     ops.argmax_parts(self.parts, self.picks)
 
   def _prefill_buffers(self, T):
