@@ -2,7 +2,7 @@
 // an fh_epilogue: the RMSNorm prologue and the epilogue chains models/llama.py puts after its matmuls.
 #pragma once
 #include <type_traits>
-#include "fh_common.h"
+#include "fh_program.h"
 
 namespace fh {
 
@@ -24,6 +24,7 @@ struct MatArgs {
   const float* cos_tab; const float* sin_tab; const int32_t* places; const int32_t* cache_rows;
   void* cache; int cache_bf16; int64_t cache_len;
   int2* argmax_parts;
+  fh_program prog;          // FH_EP_PROGRAM
 };
 
 __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
@@ -123,6 +124,10 @@ inline int epilogue_args(const char* who, const fh_epilogue* ep, int64_t K, int6
         a.cache = ep->cache; a.cache_bf16 = ep->cache_dtype == FH_BF16; a.cache_len = ep->cache_len;
         break;
       }
+      case FH_EP_PROGRAM:
+        if (int rc = check_program(who, ep->program, true)) return rc;
+        a.prog = *ep->program;
+        break;
       default: return bad(FH_EINVAL, "unknown epilogue kind");
     }
   }

@@ -226,7 +226,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
   __syncthreads();
 
   const int kind = a.kind;
-  if (a.P == 1) {  // FH_EP_STORE, FH_EP_RESIDUAL: a thread a column, 2 rows a pass; a run is 16 neighbouring lanes
+  if (a.P == 1) {  // FH_EP_STORE, FH_EP_RESIDUAL, FH_EP_PROGRAM: a thread a column, 2 rows a pass; a run is 16 lanes
     const int c = t & 127, j = c & 15;
     const int64_t run = tile_run(a, tn, c >> 4);
     const int64_t col = run * 16 + j;
@@ -236,6 +236,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
       const int64_t at = m * a.ldy + col;
       float v = Cs[r * GM_LDC + c] * rs_s[r];
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
+      if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, m, col);
       if (ok) store_out(a.y, a.y_bf16, at, v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;

@@ -143,12 +143,13 @@ __global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
 
   // the epilogue, a lane an output (or a pair of them)
   const int kind = a.kind;
-  if (kind == FH_EP_STORE || kind == FH_EP_RESIDUAL) {
+  if (kind == FH_EP_STORE || kind == FH_EP_RESIDUAL || kind == FH_EP_PROGRAM) {
     for (int i = lane; i < V; i += 64) {  // (V is a multiple of 16: a run's 16 values are 16 neighbouring lanes)
       const int b = i / (P * 16), p = (i / 16) % P, j = i % 16;
       const int64_t col = nb[p] * 16 + j, at = b * a.ldy + col;
       float v = fin[i] * (NORM ? rs[b] : 1.f);
       if (kind == FH_EP_RESIDUAL) v += a.residual[at];
+      if (kind == FH_EP_PROGRAM) v = prog_eval(a.prog, v, 0, b, col);
       store_out(a.y, a.y_bf16, at, v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;

@@ -237,7 +237,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
 
   const int kind = a.kind;
   const int64_t col_off = (int64_t)e * moe.expert_cols;
-  if (a.P == 1) {  // FH_EP_STORE / FH_EP_RESIDUAL: a thread a column of a row; a run is 16 neighbouring lanes
+  if (a.P == 1) {  // FH_EP_STORE / FH_EP_RESIDUAL / FH_EP_PROGRAM: a thread a column of a row; a run is 16 lanes
     for (int i = t; i < 16 * MB * 32; i += blockDim.x) {
       const int row = i >> 5, c = i & 31, j = c & 15;
       const int64_t run = nb[c >> 4];
@@ -246,6 +246,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       const int64_t at = (int64_t)row * a.ldy + col + col_off;
       float v = fin[row * PLD + c] * scale_s[row];
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
+      if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, row, col);
       if (ok) store_out(a.y, a.y_bf16, at, v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;

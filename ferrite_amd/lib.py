@@ -9,7 +9,13 @@ PATH = pathlib.Path(os.environ.get("FERRITE_HIP_LIB", HERE / "libferrite_hip.so"
 
 F32, BF16, BFP8, BFP4, I32 = 0, 1, 2, 3, 4
 AXIS_N, AXIS_K = 0, 1
-EP_STORE, EP_RESIDUAL, EP_SILU_GATE, EP_ROPE_KV = 0, 1, 2, 3
+EP_STORE, EP_RESIDUAL, EP_SILU_GATE, EP_ROPE_KV, EP_PROGRAM = 0, 1, 2, 3, 4
+MAX_OPS, MAX_INPUTS = 15, 8
+OPND_ACC, OPND_IMM = 24, 25
+OPS = ["add", "sub", "mul", "max", "cmplt", "cmpne", "keep", "drop", "relu", "exp", "exp2", "log", "log2", "sin", "cos",
+       "recip", "sqrt", "ftob", "itof", "ftoi", "copy"]
+OP = {name: i for i, name in enumerate(OPS)}
+REDUCE_SUM, REDUCE_MAX = 0, 1
 DTYPES = {"fp32": F32, "bf16": BF16, "bfp8": BFP8, "bfp4": BFP4, "int32": I32}
 ERRORS = {-1: ValueError, -2: NotImplementedError, -3: RuntimeError}
 
@@ -19,12 +25,19 @@ L = ctypes.c_int64
 S = ctypes.c_size_t
 
 
+class Program(ctypes.Structure):
+  """fh_program (include/ferrite_hip.h): at most 15 elementwise ops over at most 8 strided inputs."""
+  _fields_ = [("n_ops", ctypes.c_int32), ("n_inputs", ctypes.c_int32), ("op", ctypes.c_int8 * 16), ("a", ctypes.c_int8 * 16),
+              ("b", ctypes.c_int8 * 16), ("imm", ctypes.c_float * 16), ("input", P * MAX_INPUTS),
+              ("in_dtype", ctypes.c_int32 * MAX_INPUTS), ("in_stride", (L * 3) * MAX_INPUTS)]
+
+
 class Epilogue(ctypes.Structure):
   """fh_epilogue (include/ferrite_hip.h)."""
   _fields_ = [("kind", I), ("norm_w", P), ("ssq_in", P), ("eps", ctypes.c_float), ("centered", I),
               ("residual", P), ("ssq_out", P), ("split", I), ("heads", I), ("kv_heads", I), ("head_dim", I),
               ("cos_tab", P), ("sin_tab", P), ("places", P), ("cache_rows", P), ("cache", P), ("cache_dtype", I),
-              ("cache_len", L), ("argmax_parts", P)]
+              ("cache_len", L), ("argmax_parts", P), ("program", ctypes.POINTER(Program))]
 
 
 SIGNATURES = {
@@ -43,6 +56,8 @@ SIGNATURES = {
   "fh_moe_route": ([P, L, I, L, P, ctypes.c_float, I, P, I, I, I, I, P, P, P, P], I),
   "fh_moe_workspace_bytes": ([I, I, L, L], S),
   "fh_moe_experts": ([P, L, I, L, P, P, ctypes.c_float, I, I, L, P, P, I, P, P, I, P, P, P, P, P, S, P], I),
+  "fh_map": ([ctypes.POINTER(Program), P, I, L, L, L, L, L, P], I),
+  "fh_reduce": ([ctypes.POINTER(Program), I, I, L, L, L, P, I, P], I),
   "fh_argmax_rows": ([P, L, L, P, P], I),
   "fh_argmax_parts": ([P, L, L, P, P], I),
 }

@@ -1,0 +1,417 @@
+"""ferrite's lazy Tensor (ferrite/tensor.py) on an MI355X: the same surface for the block-float matmul path
+(Tensor.of, frombytes, tobytes/tolist, @ by a bfp8/bfp4 weight, cast, the elementwise ops and reductions, softmax),
+built lazily and resolved on read, every computation a kernel of libferrite_hip.so.
+
+A tensor is batch x rows x cols of bf16, fp32 or int32 (a torch tensor on the device, which is only its memory), or a
+block float (bfp8/bfp4: a matmul's B, packed by fh_bfp_pack). Ops build a tree; realize() (reading does it) compiles
+the tree under the root into as few launches as its shape allows, as ferrite's realize/_fit/_tree do (tensor.py:247-272,
+651-767):
+  - elementwise ops (and views: T, slices, expand, reshape of a stored tensor, read in place by strides) become one
+    fh_program, at most MAX_OPS (15) ops over at most 8 inputs, run by fh_map;
+  - a matmul by a block float with elementwise ops on top runs as one matmul kernel whose epilogue is that program
+    (FH_EP_PROGRAM): fh_gemv_bfp for a few rows (products exact), fh_gemm_bfp for many (x in bf16, as the chip's);
+  - a reduction (sum, max along an axis) is fh_reduce over its operand's program;
+  - what does not fit (a tree of more than 15 ops, a value read by two kernels, a matmul's operands) is realized first,
+    the heaviest shared part first.
+Programs compute in fp32 and round once, to the result's dtype (bf16 to nearest even); ferrite's SFPU rounds where its
+Dst does. int32 goes through fp32, exact below 2^24, as ferrite's does for what int32 does not do itself."""
+import ctypes, math
+import numpy as np
+import torch
+from ferrite_amd import lib, ops
+
+MAX_OPS = lib.MAX_OPS
+BFP = ("bfp8", "bfp4")
+TORCH = {"bf16": torch.bfloat16, "fp32": torch.float32, "int32": torch.int32}
+DT = {"bf16": lib.BF16, "fp32": lib.F32, "int32": lib.I32}
+ITEMSIZE = {"bf16": 2, "fp32": 4, "int32": 4}
+UNARY = ("relu", "exp", "exp2", "log", "log2", "sin", "cos", "recip", "sqrt", "ftob", "itof", "ftoi", "cast")
+BINARY = ("add", "sub", "mul", "max", "cmplt", "cmpne", "keep", "drop")
+INT32_OPS = ("add", "sub", "max", "cmplt", "cmpne", "keep", "drop")
+REDUCE = {f"{f}{ax}": (f, ax) for f in ("sum", "max") for ax in range(3)}
+
+
+class Runtime:
+  """The GPU in the place of ferrite's Runtime(chip) (ferrite/runtime.py:304-310): a device and the HIP stream every
+  launch of this runtime's tensors goes on, in order; wait() waits for them (Runtime.wait)."""
+
+  def __init__(self, device=0):
+    lib.load()
+    self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+    self.stream = torch.cuda.Stream(device=self.device) if self.device.type == "cuda" else None
+    self.launches = 0  # kernels launched (how many a realize took)
+
+  def wait(self):
+    if self.stream is not None: self.stream.synchronize()
+
+  def run(self, fn):
+    """fn() with this runtime's stream current (its library calls go on it)."""
+    self.launches += 1
+    if self.stream is None: return fn()
+    with torch.cuda.stream(self.stream):
+      return fn()
+
+
+class Tensor:
+  """batch x rows x cols (ferrite/tensor.py:14-35): a stored tensor (data) or an op on others, until realized."""
+
+  def __init__(self, rt, rows, cols, op=None, srcs=(), batch=1, dtype="bf16", args=()):
+    self.rt, self.rows, self.cols, self.batch, self.op, self.srcs, self.dtype, self.args = rt, rows, cols, batch, op, srcs, dtype, args
+    self.data = None  # a torch tensor [batch][rows][cols] (its strides may be a view's), or a BfpWeight
+
+  @property
+  def shape(self): return (self.batch, self.rows, self.cols)
+
+  def __repr__(self): return f"Tensor({self.shape}, {self.dtype}{', ' + self.op if self.op else ''})"
+
+  # ---- making and reading (ferrite/tensor.py:51-114) ------------------------------------------------------------
+  @classmethod
+  def _stored(cls, rt, t, dtype):
+    x = cls(rt, t.shape[1], t.shape[2], batch=t.shape[0], dtype=dtype)
+    x.data = t
+    return x
+
+  @classmethod
+  def full(cls, rt, rows, cols, value, dtype="bf16"): return cls.of(rt, [[value] * cols for _ in range(rows)], dtype)
+
+  @classmethod
+  def of(cls, rt, data, dtype="bf16"):
+    """From a list of rows of numbers, or a list of those (a batch), rounded to dtype (bf16: to nearest even)."""
+    assert dtype not in BFP, "a block float is made on the GPU, by cast"
+    matrices = data if isinstance(data[0][0], (list, tuple)) else [data]
+    a = torch.tensor(matrices, dtype=torch.int32 if dtype == "int32" else torch.float32)
+    return cls._stored(rt, a.to(TORCH[dtype]).to(rt.device), dtype)
+
+  @classmethod
+  def frombytes(cls, rt, rows, cols, data, batch=1, dtype="bf16"):
+    """From dtype's values in row-major order (little-endian), matrix after matrix."""
+    assert dtype not in BFP, "a block float is made on the GPU, by cast"
+    n = ITEMSIZE[dtype]
+    assert len(data) == n * batch * rows * cols, f"{len(data)} bytes for {batch} x {rows} x {cols} of {dtype}"
+    raw = torch.frombuffer(bytearray(data), dtype={2: torch.int16, 4: torch.int32}[n]).reshape(batch, rows, cols)
+    return cls._stored(rt, raw.view(TORCH[dtype]).to(rt.device), dtype)
+
+  def tobytes(self):
+    """dtype's values in row-major order, as frombytes takes them (a block float's as bf16: each of its values is one,
+    tensor._bf16s's). Waits for the launches queued."""
+    x = self.realize()
+    if x.dtype in BFP:
+      t = x.rt.run(lambda: ops.dequant(x.data))[None]
+    else:
+      if not x.data.is_contiguous(): x = (x + 0).realize()  # a view: copied by our kernel first
+      t = x.data
+    x.rt.wait()
+    t = t.cpu()
+    return (t.view(torch.int16) if t.dtype == torch.bfloat16 else t).numpy().tobytes()
+
+  def tolist(self):
+    """Rows of numbers, or a list of those if this is a batch."""
+    raw = self.tobytes()
+    if self.dtype in ("bf16", *BFP): v = (np.frombuffer(raw, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    else: v = np.frombuffer(raw, np.int32 if self.dtype == "int32" else np.float32)
+    m = v.reshape(self.batch, self.rows, self.cols).tolist()
+    return m if self.batch > 1 else m[0]
+
+  def numpy(self):
+    return np.array(self.tolist(), np.int32 if self.dtype == "int32" else np.float32).reshape(self.shape)
+
+  # ---- views: read in place by strides (ferrite/tensor.py:149-233's views and moves) ----------------------------
+  def _view(self, shape, offset, strides):
+    src = self.realize()
+    assert src.dtype not in BFP, "a block float is read only as a matmul's B"
+    t = Tensor(self.rt, shape[1], shape[2], "view", (src,), shape[0], self.dtype)
+    t.data = torch.as_strided(src.data, shape, strides, src.data.storage_offset() + offset)
+    t.op, t.srcs = None, ()
+    return t
+
+  @property
+  def T(self):
+    """The transpose of each matrix, read in place (a matmul's block-float B is transposed when packed)."""
+    if self.dtype in BFP: raise NotImplementedError("T of a block float: pack the transpose instead")
+    x = self.realize()
+    b, r, c = x.data.stride()
+    return x._view((self.batch, self.cols, self.rows), 0, (b, c, r))
+
+  def __getitem__(self, key):
+    """x[b], one matrix of a batch; x[rows, cols] or x[batch, rows, cols] with slices (any positive step): a view."""
+    x = self.realize()
+    if isinstance(key, int):
+      b, r, c = x.data.stride()
+      return x._view((1, self.rows, self.cols), key * b, (b, r, c))
+    key = (slice(None),) * (3 - len(key)) + tuple(key)
+    rng = [range(*k.indices(n)) for k, n in zip(key, self.shape)]
+    assert all(g.step > 0 and len(g) for g in rng), "slices of positive steps, not empty"
+    st = x.data.stride()
+    return x._view(tuple(map(len, rng)), sum(g.start * s for g, s in zip(rng, st)), tuple(g.step * s for g, s in zip(rng, st)))
+
+  def expand(self, *shape):  # dimensions of 1 repeated (a stride of 0), missing ones in front being 1
+    shape = (1,) * (3 - len(shape)) + shape
+    assert all(n in (m, 1) for n, m in zip(self.shape, shape)), f"cannot expand {self.shape} to {shape}"
+    x = self.realize()
+    return x._view(shape, 0, tuple(0 if n == 1 and m > 1 else s for n, m, s in zip(self.shape, shape, x.data.stride())))
+
+  def reshape(self, *shape):  # up to three sizes, missing ones in front being 1
+    shape = (1,) * (3 - len(shape)) + shape
+    assert math.prod(shape) == math.prod(self.shape), f"cannot reshape {self.shape} to {shape}"
+    x = self.realize()
+    if not x.data.is_contiguous(): x = (x + 0).realize()  # a copy first
+    return x._view(shape, 0, (shape[1] * shape[2], shape[2], 1))
+
+  # ---- elementwise (ferrite/tensor.py:300-360) --------------------------------------------------------------------
+  def _unary(self, op):
+    if self.dtype == "int32" and op != "relu": return self.float()._unary(op)
+    return Tensor(self.rt, self.rows, self.cols, op, (self,), self.batch, self.dtype)
+
+  def _binop(self, op, x, reverse=False):
+    """numpy's broadcasting; a number is the op's immediate; different dtypes meet in fp32, and so does int32 for what
+    it does not do itself."""
+    if not isinstance(x, Tensor):
+      num = float(x)
+      dtype = "fp32" if self.dtype == "int32" and isinstance(x, float) else self.dtype
+      a = self if dtype == self.dtype else self.float()
+      return Tensor(self.rt, self.rows, self.cols, op, (a,), self.batch, dtype, args=(num, reverse))
+    a, b = (x, self) if reverse else (self, x)
+    if a.dtype != b.dtype or (a.dtype == "int32" and op not in INT32_OPS): a, b = a.float(), b.float()
+    assert all(n == m or 1 in (n, m) for n, m in zip(a.shape, b.shape)), f"cannot broadcast {a.shape} with {b.shape}"
+    batch, rows, cols = map(max, a.shape, b.shape)
+    return Tensor(self.rt, rows, cols, op, (a, b), batch, a.dtype)
+
+  def cast(self, dtype):
+    """To another dtype; to a block float, packed at once (fh_bfp_pack, Tensor.cast's bfp4_kernel / packer)."""
+    if dtype == self.dtype: return self
+    if dtype in BFP:
+      x = self.realize()
+      assert x.batch == 1, "a block float of one matrix"
+      if x.dtype == "int32" or not x.data.is_contiguous(): x = (x.float() if x.dtype == "int32" else x + 0).realize()
+      out = Tensor(self.rt, self.rows, self.cols, batch=1, dtype=dtype)
+      out.data = x.rt.run(lambda: ops.pack(x.data[0], dtype))
+      return out
+    if self.dtype in BFP:  # a block float's values (each a bf16 value)
+      b = Tensor(self.rt, self.rows, self.cols, batch=1, dtype="bf16")
+      b.data = self.rt.run(lambda: ops.dequant(self.data))[None]
+      return b.cast(dtype)
+    return Tensor(self.rt, self.rows, self.cols, "cast", (self,), self.batch, dtype)
+
+  def float(self): return self.cast("fp32")
+  def bfloat16(self): return self.cast("bf16")
+  def exp2(self): return self._unary("exp2")
+  def log2(self): return self._unary("log2")
+  def sin(self): return self._unary("sin")
+  def sqrt(self): return self._unary("sqrt")
+  def reciprocal(self): return self._unary("recip")
+  def exp(self): return self._unary("exp")
+  def log(self): return self._unary("log")
+  def cos(self): return self._unary("cos")
+  def relu(self): return self._unary("relu")
+  def rsqrt(self): return self.sqrt().reciprocal()
+  def maximum(self, x): return self._binop("max", x)
+  def minimum(self, x): return -((-self).maximum(-x))
+  def where(self, x, y):  # x where self is not 0, else y
+    dtype = next((t.dtype for t in (x, y) if isinstance(t, Tensor)), self.dtype)
+    c = self if self.dtype == dtype else self.ne(0).cast(dtype)
+    return c._binop("keep", x) + c._binop("drop", y)
+  def __add__(self, x): return self._binop("add", x)
+  def __sub__(self, x): return self._binop("sub", x)
+  def __mul__(self, x): return self._binop("mul", x)
+  def __rsub__(self, x): return self._binop("sub", x, True)
+  __radd__, __rmul__ = __add__, __mul__
+  def __truediv__(self, x): return self * (1 / x if isinstance(x, (int, float)) else x.reciprocal())
+  def __neg__(self): return 0 - self if self.dtype == "int32" else self * -1
+  def __lt__(self, x): return self._binop("cmplt", x)
+  def __gt__(self, x): return self._binop("cmplt", x, True)
+  def __ge__(self, x): return 1 - (self < x)
+  def __le__(self, x): return 1 - (self > x)
+  def ne(self, x): return self._binop("cmpne", x)
+  def eq(self, x): return 1 - self.ne(x)
+  __ne__, __eq__ = ne, eq
+  def __hash__(self): return id(self)
+  def sigmoid(self): return (1 + (-self).exp()).reciprocal()
+  def silu(self): return self * self.sigmoid()
+  def gelu(self):
+    k = 2 * math.sqrt(2 / math.pi)
+    return self * (1 + (self * (self * self * (-0.044715 * k) - k)).exp()).reciprocal()
+
+  # ---- reductions (ferrite/tensor.py:362-372, 430-440) -------------------------------------------------------------
+  def sum(self, axis=None): return self._reduce("sum", axis)
+  def max(self, axis=None): return self._reduce("max", axis)
+
+  def _reduce(self, f, axis):
+    if self.dtype == "int32": return self.float()._reduce(f, axis).cast("int32")
+    if axis is None: return self._reduce(f, 0)._reduce(f, 1)._reduce(f, 2)
+    shape = [1 if ax == axis % 3 else s for ax, s in enumerate(self.shape)]
+    if shape == list(self.shape): return self
+    return Tensor(self.rt, shape[1], shape[2], f"{f}{axis % 3}", (self,), shape[0], self.dtype)
+
+  def mean(self, axis=None):
+    s = self.sum(axis)
+    return s * (math.prod(s.shape) / math.prod(self.shape))
+
+  def softmax(self, axis=-1):  # the max first, so exp stays in range
+    e = (self - self.max(axis)).exp()
+    return e / e.sum(axis)
+
+  def log_softmax(self, axis=-1):
+    m = self - self.max(axis)
+    return m - m.exp().sum(axis).log()
+
+  def layernorm(self, axis=-1, eps=1e-5):
+    c = self - self.mean(axis)
+    return c * ((c * c).mean(axis) + eps).rsqrt()
+
+  # ---- matmul (ferrite/tensor.py:443-485) ----------------------------------------------------------------------------
+  def __matmul__(self, x): return self.matmul(x)
+
+  def matmul(self, x, dtype=None):
+    """self (1 x rows x K) @ x (K x N, a block float: bfp8 or bfp4, cast once), written as dtype: bf16, or fp32 if
+    self is, unless said. fp32 rows, a few, go through the exact-product GEMV; otherwise the matrix cores take self's
+    values in bf16, as ferrite's chip does (bf16 rows: exact products too); the elementwise ops on top of it run in
+    the same kernel."""
+    if x.dtype not in BFP: raise NotImplementedError("matmul: B is a block float (bfp8 or bfp4) on this runtime")
+    assert self.batch == 1 and self.cols == x.rows and self.dtype != "int32", f"{self.shape} @ {x.shape}"
+    return Tensor(self.rt, self.rows, x.cols, "matmul", (self, x.realize()), 1, dtype or ("fp32" if self.dtype == "fp32" else "bf16"))
+
+  # ---- realizing ----------------------------------------------------------------------------------------------------
+  def realize(self):
+    """Compute it now (if it is an op), into memory of its own; returns it, realized."""
+    if self.data is not None: return self
+    if self.op in REDUCE:
+      f, axis = REDUCE[self.op]
+      src = self.srcs[0]
+      prog, inputs = _fit_program(src, src.shape, allow_acc=False)
+      out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
+      p = _cprogram(prog, inputs)
+      self.rt.run(lambda: lib.call("fh_reduce", ctypes.byref(p), lib.REDUCE_MAX if f == "max" else lib.REDUCE_SUM, axis,
+                                   *src.shape, ops._ptr(out), DT[self.dtype], ops._stream()))
+      self._done(out)
+      return self
+    prog, inputs = _fit_program(self, self.shape, allow_acc=True)
+    mm = next((t for t in _walk(self) if getattr(t, "_acc", False)), None)
+    out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
+    p = _cprogram(prog, inputs)
+    if mm is not None:
+      mm._acc = False
+      a, w = mm.srcs[0].realize(), mm.srcs[1].data
+      if a.data.stride(2) != 1: a = (a + 0).realize()  # rows contiguous (our copy kernel)
+      x = a.data[0]
+      y = out[0]
+      program = [p]
+      ep = ops.epilogue(lib.EP_PROGRAM)
+      ep.program = ctypes.pointer(p)
+      ep.keep.append(program)
+      if w.K % 32 or (a.dtype == "fp32" and a.rows <= 8):  # fp32 rows, or a K the matrix cores do not take: the
+        if x.dtype != torch.float32: x = a.float().realize().data[0]  # exact-product GEMV
+        self.rt.run(lambda: ops.gemv(x, w, ep, out=y))
+      else:  # the matrix cores (bf16 rows go in as they are: their products are exact too)
+        self.rt.run(lambda: ops.gemm(x, w, ep, out=y))
+    else:
+      ld = out.stride()
+      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[self.dtype], *self.shape, ld[0], ld[1], ops._stream()))
+    self._done(out)
+    return self
+
+  def _done(self, data):
+    self.data, self.op, self.srcs, self.args = data, None, (), ()
+
+
+def _walk(t, seen=None):
+  """The unrealized nodes under t (t first), each once."""
+  seen = set() if seen is None else seen
+  if t.data is not None or id(t) in seen: return
+  seen.add(id(t))
+  yield t
+  for s in t.srcs: yield from _walk(s, seen)
+
+
+def _ops(t, acc_ok):
+  """How many program ops t's tree would take, counting each shared node once and stopping at what realizes apart."""
+  n = 0
+  for u in _walk(t):
+    if u.op in REDUCE or (u.op == "matmul" and not acc_ok): continue
+    if u.op == "matmul": n += 1; continue
+    n += 1
+  return n
+
+
+def _fit_program(root, shape, allow_acc):
+  """The program computing root's elementwise tree at each element of shape, its inputs; realizing first what does
+  not fit: reductions, matmuls other than one (the epilogue's acc), and, while the tree holds more than MAX_OPS ops,
+  the biggest subtree two ops read, else the heaviest operand (ferrite/tensor.py:651-669's _fit)."""
+  while True:
+    readers = {}
+    for u in _walk(root):
+      for s in u.srcs: readers[id(s)] = readers.get(id(s), 0) + 1
+    for u in list(_walk(root)):  # reductions (a reduction's own operand too) and every matmul but the root's chain's
+      if u.op in REDUCE: u.realize()  # first are realized apart
+    accs = [u for u in _walk(root) if u.op == "matmul"]
+    for i, u in enumerate(accs):
+      if not allow_acc or i > 0 or readers.get(id(u), 0) > 1 or u.shape != tuple(shape): u.realize()
+    n = _ops(root, allow_acc)
+    if n <= MAX_OPS: break
+    lazy = [u for u in _walk(root)][1:]
+    shared = [u for u in lazy if readers.get(id(u), 0) > 1 and _ops(u, False) <= MAX_OPS]
+    u = max(shared, key=lambda v: _ops(v, False)) if shared else root
+    while _ops(u, False) > MAX_OPS: u = max((s for s in u.srcs if s.data is None), key=lambda v: _ops(v, False))
+    u.realize()
+  prog, inputs, regs = [], [], {"root": root}
+  _emit(root, shape, prog, inputs, regs)
+  if not prog: prog.append(("copy", _operand(root, shape, prog, inputs, regs), lib.OPND_IMM, 0.0))
+  return prog, inputs
+
+
+def _operand(t, shape, prog, inputs, regs):
+  """t's operand code: an earlier op's register, an input (a stored tensor, broadcast by strides), or acc."""
+  if t.data is not None:
+    for k, (u, _) in enumerate(inputs):
+      if u is t: return 16 + k
+    assert len(inputs) < lib.MAX_INPUTS, "a program reads at most 8 inputs"
+    st = [0 if n == 1 and m > 1 else s for n, m, s in zip(t.shape, shape, t.data.stride())]
+    inputs.append((t, st))
+    return 16 + len(inputs) - 1
+  return _emit(t, shape, prog, inputs, regs)
+
+
+def _emit(t, shape, prog, inputs, regs):
+  """Emits t's ops (operands first) into prog; returns the code of t's value."""
+  if id(t) in regs: return regs[id(t)]
+  if t.op == "matmul":
+    t._acc = True
+    regs[id(t)] = lib.OPND_ACC
+    return lib.OPND_ACC
+  if t.data is not None or t.op is None: return _operand(t, shape, prog, inputs, regs)
+  op = t.op
+  if op == "cast" and t is not regs["root"] and t.dtype != "fp32":  # a rounding below the root: realized first, as
+    t.realize()                                                     # ferrite's casts below the root are
+    return _operand(t, shape, prog, inputs, regs)
+  if op == "cast":  # rounding happens at the result's store; a cast to int32 truncates toward 0 there
+    a = _operand(t.srcs[0], shape, prog, inputs, regs)
+    prog.append(("ftoi" if t.dtype == "int32" and t.srcs[0].dtype != "int32" else "copy", a, lib.OPND_IMM, 0.0))
+  elif op in UNARY:
+    a = _operand(t.srcs[0], shape, prog, inputs, regs)
+    prog.append((op, a, lib.OPND_IMM, 0.0))
+  elif op in BINARY and len(t.srcs) == 1:  # with a number
+    num, reverse = t.args
+    a = _operand(t.srcs[0], shape, prog, inputs, regs)
+    prog.append((op, lib.OPND_IMM, a, num) if reverse else (op, a, lib.OPND_IMM, num))
+  elif op in BINARY:
+    a = _operand(t.srcs[0], shape, prog, inputs, regs)
+    b = _operand(t.srcs[1], shape, prog, inputs, regs)
+    prog.append((op, a, b, 0.0))
+  else:
+    raise NotImplementedError(f"op {op}")
+  regs[id(t)] = len(prog) - 1
+  return regs[id(t)]
+
+
+def _cprogram(prog, inputs):
+  """The fh_program of an emitted program."""
+  assert 1 <= len(prog) <= MAX_OPS, f"{len(prog)} ops"
+  p = lib.Program()
+  p.n_ops, p.n_inputs = len(prog), len(inputs)
+  for i, (op, a, b, imm) in enumerate(prog):
+    p.op[i], p.a[i], p.b[i], p.imm[i] = lib.OP[op], a, b, imm
+  for k, (t, st) in enumerate(inputs):
+    p.input[k] = t.data.data_ptr()
+    p.in_dtype[k] = DT[t.dtype]
+    for j in range(3): p.in_stride[k][j] = st[j]
+  p.keep = [t.data for t, _ in inputs]
+  return p

@@ -79,6 +79,31 @@ int fh_bfp_dequant(const void* mant, const uint8_t* exps, int64_t K, int64_t N, 
 #define FH_EP_RESIDUAL 1   /* y = residual + acc, and the sums of squares of y by 16 columns into ssq_out (if set) */
 #define FH_EP_SILU_GATE 2  /* W's columns are [gate | up], each `split` wide: y[:, j] = silu(gate_j) * up_j, j < split */
 #define FH_EP_ROPE_KV 3    /* W's columns are q, k and v heads: RoPE on q's and k's, q into y, k and v into the cache */
+#define FH_EP_PROGRAM 4    /* y = program(acc): a chain of elementwise ops on the matmul's result (fh_program below) */
+
+/* ---- elementwise programs: the ops ferrite fuses into one kernel (Tensor.realize's tree, ferrite/tensor.py:247-272,
+ * 708-767; fused_kernel's SFPU programs, ferrite/compiler.py:274-340), at most FH_MAX_OPS of them ----------------
+ * Op i computes r_i = op(a, b) in fp32 from operands: r_j (j < i), input k (its element at the output's (batch, row,
+ * column) by its strides; a stride of 0 broadcasts), the matmul's result (an epilogue's), or the op's immediate. The
+ * program's value is its last op's. keep/drop are where()'s halves: a if b != 0 else 0, and a if b == 0 else 0. */
+#define FH_MAX_OPS 15
+#define FH_MAX_INPUTS 8
+#define FH_OPND_IN(k) (16 + (k))   /* operand codes: 0..14 an op's result, 16..23 an input */
+#define FH_OPND_ACC 24             /* the matmul's result */
+#define FH_OPND_IMM 25             /* the op's immediate */
+enum {
+  FH_OP_ADD = 0, FH_OP_SUB, FH_OP_MUL, FH_OP_MAX, FH_OP_CMPLT, FH_OP_CMPNE, FH_OP_KEEP, FH_OP_DROP,
+  FH_OP_RELU, FH_OP_EXP, FH_OP_EXP2, FH_OP_LOG, FH_OP_LOG2, FH_OP_SIN, FH_OP_COS, FH_OP_RECIP, FH_OP_SQRT,
+  FH_OP_FTOB, FH_OP_ITOF, FH_OP_FTOI, FH_OP_COPY
+};
+typedef struct fh_program {
+  int32_t n_ops, n_inputs;
+  int8_t op[16], a[16], b[16];
+  float imm[16];
+  const void* in[FH_MAX_INPUTS];
+  int32_t in_dtype[FH_MAX_INPUTS];        /* FH_F32, FH_BF16 or FH_I32 */
+  int64_t in_stride[FH_MAX_INPUTS][3];    /* elements between batches, rows, columns */
+} fh_program;
 
 typedef struct fh_epilogue {
   int kind;                 /* FH_EP_* */
@@ -106,6 +131,8 @@ typedef struct fh_epilogue {
   /* FH_EP_STORE: each row's largest value of each run of 16 columns and its column (the first of equals), as
    * (float, int32) pairs [batch][N/16], for fh_argmax_parts: greedy decoding's pick without a second pass over y */
   void* argmax_parts;
+  /* FH_EP_PROGRAM: the program, evaluated at each output (batch row, column) with the matmul's result as its acc */
+  const struct fh_program* program;
 } fh_epilogue;
 
 /* y (dtype y_dtype, row stride ldy) from x @ W and the epilogue. x: fp32. w_mant/w_exps: a packed [K][N] weight
@@ -184,6 +211,21 @@ int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim, const flo
                    int centered, int experts, int64_t ffn, const void* gu_mant, const uint8_t* gu_exps, int gu_fmt,
                    const void* down_mant, const uint8_t* down_exps, int down_fmt, const float* dense, float* y,
                    const float* residual, float* ssq_out, void* workspace, size_t ws_bytes, void* stream);
+
+/* ---- lazy tensors' kernels (ferrite/tensor.py: elementwise trees, reductions) ---------------------------------- */
+
+/* out[b][r][c] = program at (b, r, c), out's dtype FH_F32, FH_BF16 (nearest even) or FH_I32; out rows ldo apart,
+ * batches ldb apart. Replaces fused_kernel for an elementwise tree (ferrite/compiler.py:699). */
+int fh_map(const fh_program* program, void* out, int out_dtype, int64_t batch, int64_t rows, int64_t cols, int64_t ldb,
+           int64_t ldo, void* stream);
+
+/* The program's values summed (FH_REDUCE_SUM) or their largest (FH_REDUCE_MAX) along an axis of (batch, rows, cols)
+ * (0, 1 or 2), out holding the result with that axis 1 (ferrite/tensor.py's _reduce, 362-368; FOLDS and COMBINE,
+ * ferrite/compiler.py:345-348). fp32 sums in a fixed order. */
+#define FH_REDUCE_SUM 0
+#define FH_REDUCE_MAX 1
+int fh_reduce(const fh_program* program, int kind, int axis, int64_t batch, int64_t rows, int64_t cols, void* out,
+              int out_dtype, void* stream);
 
 /* For each row of x[rows][n] (fp32), its largest value's column (the first of equals), into ids[rows]: greedy
  * decoding's pick (models/llama.py:792, numpy's argmax). */

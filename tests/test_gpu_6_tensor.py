@@ -1,0 +1,178 @@
+"""ferrite's lazy Tensor surface on the GPU (ferrite_amd.tensor) against numpy, the way the reference's test_sim.py
+checks its Tensor on ttsim: values in and out (bf16 to nearest even), elementwise trees fused into one launch, the
+reductions and what is built from them, matmul by a block float with its elementwise chain in the same kernel, casts to
+block floats read back as the oracle decodes them. Programs compute in fp32 and round once, so a bf16 result is within
+2^-8 of numpy's float64 value of the same expression on the same (bf16) inputs. Reference tests of the same:
+test_elementwise / test_reduce / test_softmax / test_matmul_random (test/test_sim.py)."""
+import numpy as np
+import pytest
+import torch
+from oracle import bfp as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rt(cuda):
+  from ferrite_amd import tensor
+  return tensor.Runtime(0)
+
+
+def Tn():
+  from ferrite_amd import tensor
+  return tensor.Tensor
+
+
+def close(got, want, rel, what):
+  got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+  err = np.abs(got - want)
+  bound = rel * np.maximum(np.abs(want), np.abs(want).max() * 1e-3) + 1e-30
+  assert (err <= bound).all(), (what, float((err / bound).max()))
+
+
+def test_values_in_and_out(rt):
+  rng = np.random.default_rng(61)
+  a = rng.normal(0, 3, (3, 5, 7)).astype(np.float32)
+  t = Tn().of(rt, a.tolist(), "bf16")
+  assert np.array_equal(np.array(t.tolist(), np.float32), O.bf16(a))
+  f = Tn().of(rt, a[0].tolist(), "fp32")
+  assert np.array_equal(np.array(f.tolist(), np.float32), a[0])
+  i = Tn().frombytes(rt, 2, 3, np.arange(6, dtype=np.int32).tobytes(), dtype="int32")
+  assert i.tolist() == [[0, 1, 2], [3, 4, 5]] and i.tobytes() == np.arange(6, dtype=np.int32).tobytes()
+
+
+def test_elementwise_tree_is_one_launch(rt):
+  rng = np.random.default_rng(62)
+  x = O.bf16(rng.normal(0, 1, (1, 64, 96)))
+  y = O.bf16(rng.normal(0, 1, (1, 1, 96)))        # a row, broadcast down the rows
+  c = O.bf16(rng.normal(0, 1, (1, 64, 1)))        # a column, broadcast along the rows
+  X, Y, C = (Tn().of(rt, a[0].tolist()) for a in (x, y, c))
+  z = ((X * Y + C).sigmoid() * X - (X - 0.5).relu()).maximum(Y * 0.25)
+  before = rt.launches
+  got = z.numpy()
+  assert rt.launches - before == 1, rt.launches - before
+  s = 1 / (1 + np.exp(-(x.astype(np.float64) * y + c)))
+  want = np.maximum(s * x - np.maximum(x - 0.5, 0), y * 0.25)
+  close(got, O.bf16(want), 2 ** -8, "tree")
+
+
+@pytest.mark.parametrize("name", ["exp", "log", "sqrt", "sin", "cos", "reciprocal", "silu", "gelu", "exp2", "log2"])
+def test_unary(rt, name):
+  rng = np.random.default_rng(63)
+  a = O.bf16(np.abs(rng.normal(0, 2, (16, 48))) + 0.1)
+  f = {"exp": np.exp, "log": np.log, "sqrt": np.sqrt, "sin": np.sin, "cos": np.cos, "reciprocal": lambda v: 1 / v,
+       "silu": lambda v: v / (1 + np.exp(-v)), "exp2": np.exp2, "log2": np.log2,
+       "gelu": lambda v: 0.5 * v * (1 + np.tanh(np.sqrt(2 / np.pi) * (v + 0.044715 * v ** 3)))}[name]
+  got = getattr(Tn().of(rt, a.tolist(), "fp32"), name)().numpy()[0]
+  close(got, f(a.astype(np.float64)), 1e-5, name)
+
+
+def test_where_and_comparisons(rt):
+  a = np.array([[1.0, -2.0, 3.0, 0.0]], np.float32)
+  b = np.array([[1.0, 2.0, -3.0, 0.0]], np.float32)
+  A, B = Tn().of(rt, a.tolist(), "fp32"), Tn().of(rt, b.tolist(), "fp32")
+  assert (A < B).tolist() == [[0.0, 1.0, 0.0, 0.0]]
+  assert (A >= B).tolist() == [[1.0, 0.0, 1.0, 1.0]]
+  assert A.eq(B).tolist() == [[1.0, 0.0, 0.0, 1.0]]
+  assert (A > 0).where(A, B * 10).tolist() == [[1.0, 20.0, 3.0, 0.0]]
+  assert A.minimum(B).tolist() == [[1.0, -2.0, -3.0, 0.0]]
+
+
+def test_int32(rt):
+  a = Tn().of(rt, [[5, -7, 2**20]], "int32")
+  b = Tn().of(rt, [[3, 3, 1]], "int32")
+  assert (a + b).tolist() == [[8, -4, 2**20 + 1]] and (a - b).tolist() == [[2, -10, 2**20 - 1]]
+  assert a.maximum(b).tolist() == [[5, 3, 2**20]] and (a + b).dtype == "int32"
+  assert (a * 2).tolist() == [[10, -14, 2**21]]
+
+
+@pytest.mark.parametrize("axis", [0, 1, 2, None])
+def test_reductions(rt, axis):
+  rng = np.random.default_rng(64)
+  a = rng.normal(0, 1, (3, 40, 300)).astype(np.float32)
+  t = Tn().of(rt, a.tolist(), "fp32")
+  kw = dict(axis=axis, keepdims=True) if axis is not None else {}
+  n = a.size if axis is None else a.shape[axis]
+  absum = np.abs(a.astype(np.float64)).sum(**kw).reshape(-1)
+  for f, ref in (("sum", np.sum), ("max", np.max), ("mean", np.mean)):
+    got = getattr(t, f)(axis).numpy().reshape(-1)
+    want = ref(a.astype(np.float64), **kw).reshape(-1)
+    if f == "max":
+      assert np.array_equal(got, want), (f, axis)  # (a largest is one of the values, exactly)
+    else:  # fp32 sums in order: within n 2^-24 of the sum of magnitudes
+      bound = n * 2.0 ** -24 * absum / (n if f == "mean" else 1) + 1e-30
+      assert (np.abs(got - want) <= bound).all(), (f, axis, float((np.abs(got - want) / bound).max()))
+
+
+def test_softmax_family(rt):
+  rng = np.random.default_rng(65)
+  a = rng.normal(0, 3, (1, 33, 1000)).astype(np.float32)
+  t = Tn().of(rt, a[0].tolist(), "fp32")
+  e = np.exp(a - a.max(-1, keepdims=True))
+  close(t.softmax().numpy(), e / e.sum(-1, keepdims=True), 1e-5, "softmax")
+  close(t.log_softmax().numpy(), np.log(e / e.sum(-1, keepdims=True)), 1e-5, "log_softmax")
+  c = a - a.mean(-1, keepdims=True)
+  close(t.layernorm().numpy(), c / np.sqrt((c * c).mean(-1, keepdims=True) + 1e-5), 1e-4, "layernorm")
+
+
+@pytest.mark.parametrize("rows", [1, 16, 200])
+def test_matmul_and_its_chain(rt, rows):
+  # bf16 rows @ a bfp8 weight, then bias, relu and a row softmax: the matmul and its elementwise chain one kernel,
+  # the softmax's two reductions and its division three more
+  rng = np.random.default_rng(66)
+  K, N = 576, 1536
+  x = O.bf16(rng.normal(0, 1, (rows, K)))
+  w = rng.normal(0, 0.02, (K, N)).astype(np.float32)
+  bias = O.bf16(rng.normal(0, 0.1, (1, N)))
+  W = Tn().of(rt, w.tolist(), "fp32").cast("bfp8")
+  X, Bias = Tn().of(rt, x.tolist()), Tn().of(rt, bias.tolist())
+  h = (X @ W + Bias).relu()
+  before = rt.launches
+  hv = h.float().realize()
+  assert rt.launches - before == 1
+  wv = O.bfp(w)
+  want = np.maximum(x.astype(np.float64) @ wv + bias, 0)
+  # (x is bf16 already: exact products on either path, fp32 sums): within fp32 summation's error, 1e-5 of sum |x w|
+  bound = 1e-5 * (np.abs(x) @ np.abs(wv) + np.abs(bias)) + 1e-30
+  err = np.abs(hv.numpy()[0] - want)
+  assert (err <= bound).all(), ("matmul", rows, float((err / bound).max()))
+  # the softmax of an fp32 matmul's chain: its two reductions realize the matmul apart (fp32, so nothing rounds to
+  # bf16 between them); within exp's growth of the sums' fp32 error
+  s = (X.matmul(W, "fp32") + Bias).relu().softmax().numpy()[0]
+  e = np.exp(want - want.max(-1, keepdims=True))
+  close(s, e / e.sum(-1, keepdims=True), 1e-4, ("softmax", rows))
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+def test_cast_to_block_float(rt, fmt):
+  # Tensor.cast("bfp8"/"bfp4") read back as bf16 (tensor._bf16s): the oracle's values, bit for bit
+  rng = np.random.default_rng(67)
+  a = O.bf16(rng.normal(0, 1, (64, 96)) * np.exp(rng.normal(0, 2, (64, 96))))
+  t = Tn().of(rt, a.tolist()).cast(fmt)
+  got = np.frombuffer(t.tobytes(), np.uint16).reshape(64, 96)
+  q, top = O.bfp_parts(a, fmt)
+  assert np.array_equal(got, O.exact_bf16(q, top, fmt))
+
+
+def test_views(rt):
+  rng = np.random.default_rng(68)
+  a = rng.normal(0, 1, (2, 6, 8)).astype(np.float32)
+  t = Tn().of(rt, a.tolist(), "fp32")
+  assert np.array_equal(t.T.numpy(), a.transpose(0, 2, 1))
+  assert np.array_equal(t[1].numpy(), a[1:2])
+  assert np.array_equal(t[:, 1:5:2, ::3].numpy(), a[:, 1:5:2, ::3])
+  assert np.array_equal(t[0][:, :, 0:1].expand(1, 6, 8).numpy(), np.broadcast_to(a[0:1, :, 0:1], (1, 6, 8)))
+  assert np.array_equal(t.reshape(4, 24).numpy(), a.reshape(1, 4, 24))
+  assert np.array_equal((t.T * 2).numpy(), a.transpose(0, 2, 1) * 2)
+
+
+def test_long_tree_in_parts(rt):
+  # more than MAX_OPS ops: realized in parts, the value the same
+  rng = np.random.default_rng(69)
+  a = rng.normal(0, 1, (4, 32)).astype(np.float32)
+  t = Tn().of(rt, a.tolist(), "fp32")
+  z, want = t, a.astype(np.float64)
+  for i in range(20):
+    z = (z * 0.9 + 0.1).relu() if i % 2 else z * 1.01 - 0.02
+    want = np.maximum(want * 0.9 + 0.1, 0) if i % 2 else want * 1.01 - 0.02
+  close(z.numpy()[0], want, 1e-5, "long")
