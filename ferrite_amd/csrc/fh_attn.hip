@@ -1,18 +1,21 @@
-// Decode attention over a KV cache, flash-decoding style, in two kernels. The first: a workgroup (two waves) takes a
-// chunk of 128 cache rows of one batch row for one query head (grouped-query: its key head is h / (heads / kv_heads);
-// the query heads that share a key head read the same rows, which the Infinity Cache serves after the first); each
-// lane scores one row (its keys' loads all in flight), the wave takes its largest score and sum of exps, then each
-// lane accumulates p * v for its dimensions (the wave's 64 rows of values loaded one row per instruction, all in
-// flight); the waves meet in LDS and the chunk's (max, sum, p v) goes to the workspace, or, when the row's keys fit one
-// chunk, o itself. The second kernel combines the chunks of each (row, head) by exp(max - the largest). A kernel
-// boundary, not a fence, orders the two. A row reads only the cache rows its place reaches.
+// Decode attention over a KV cache, flash-decoding style, in two kernels. The first: a workgroup takes a chunk of 64
+// cache rows of one batch row for one key head, with a wave for each query head that reads it (grouped-query: query
+// head h reads key head h / (heads / kv_heads)). Its threads load the chunk's keys and values into LDS once (each
+// byte of the cache read once from HBM; every load of the chunk and of q in flight together, one memory round trip);
+// each wave then scores the 64 rows against its head's q (a lane a row), takes their largest score and sum of exps,
+// and accumulates p * v (a lane HD / 64 dimensions, four rows' p a broadcast read). A row whose keys fit one chunk
+// writes o directly; otherwise each chunk's (p v, max, sum) goes to the workspace, and the second kernel combines the
+// chunks of each (row, head): a thread a chunk's statistics and a dimension's values, all loaded in one round with the
+// row's place, one exp(max - the largest) a thread. A kernel boundary, not a fence, orders the two: on MI355X an
+// agent-scope release (an L2 write-back on each XCD) and a counter cost more than the ~1.4 us boundary. A row reads
+// only the cache rows its place reaches.
 #include <math.h>
 #include "fh_common.h"
 
 namespace fh {
 
-constexpr int ATT_WAVES = 2;                 // waves a workgroup, 64 cache rows each
-constexpr int ATT_CHUNK = 64 * ATT_WAVES;    // cache rows a workgroup
+constexpr int ATT_CHUNK = 64;                // cache rows a workgroup (a lane a row)
+constexpr int ATT_REP = 16;                  // query heads a key head, at most (a wave each)
 
 struct AttArgs {
   const float* q; const void* cache; int64_t cache_len;
@@ -32,163 +35,199 @@ __device__ inline void row_range(const AttArgs& a, int b, int64_t& row0, int64_t
   length = length < 1 ? 1 : (length > room ? room : length);
 }
 
+// LDS a workgroup: keys and values [64][row + 16 bytes], the heads' q [rep][HD] fp32, their p [rep][64]
+__host__ __device__ constexpr int att_row_bytes(int hd, int es) { return hd * es + 16; }
+static size_t att_lds(int hd, int es, int rep) {
+  return (size_t)2 * ATT_CHUNK * att_row_bytes(hd, es) + (size_t)rep * hd * 4 + (size_t)rep * ATT_CHUNK * 4;
+}
+
 template <int HD, bool BF>
-__global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(AttArgs a) {
-  constexpr int DL = HD / 64;
-  const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;  // h: the query head (its key head h / rep)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kvh = h / (a.heads / a.kv_heads);
+__global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(AttArgs a) {
+  constexpr int DL = HD / 64;                  // dimensions a lane (p v, the combine)
+  constexpr int ES = BF ? 2 : 4;               // bytes an element
+  constexpr int RW = att_row_bytes(HD, ES);    // (16 more than the row: a lane's 16-byte reads of its own row spread
+                                               // over the banks)
+  extern __shared__ __attribute__((aligned(16))) char att_smem[];
+  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int rep = a.heads / a.kv_heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthreads = 64 * rep;
+  const int h = kvh * rep + wave;              // this wave's query head
   int64_t row0, length;
   row_range(a, b, row0, length);
   const int nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);
   if (chunk >= nchunks) return;  // past the row's place
+  const int64_t c0 = (int64_t)chunk * ATT_CHUNK;
+  const int n = (int)(length - c0 < ATT_CHUNK ? length - c0 : ATT_CHUNK);  // rows of this chunk (>= 1)
+  char* ks = att_smem;
+  char* vs = att_smem + ATT_CHUNK * RW;
+  float* qs = (float*)(att_smem + 2 * ATT_CHUNK * RW);
+  float* ps = qs + rep * HD + wave * ATT_CHUNK;  // this wave's p
 
-  __shared__ float qs[HD];
-  __shared__ float ps[ATT_WAVES][64];
-  __shared__ float wm[ATT_WAVES], wl[ATT_WAVES];
-  __shared__ float wo[ATT_WAVES][HD];
-  const int64_t w0 = (int64_t)chunk * ATT_CHUNK + 64 * wave;  // the wave's first row
-  const int n = (int)(length - w0 < 64 ? (length - w0 > 0 ? length - w0 : 0) : 64);
-  const int64_t t = w0 + (lane < n ? lane : (n > 0 ? n - 1 : 0));  // (a lane past the rows reads the last, unused)
-  const bool valid = lane < n;
-
-  // every load at once: q, the lane's row of keys, and the wave's 64 rows of values (a lane its DL dimensions)
-  float qv[(HD + 64 * ATT_WAVES - 1) / (64 * ATT_WAVES)];
+  // the chunk's keys and values into LDS, 16 bytes a thread a piece, and the heads' q: every load issued before any
+  // LDS store (rows past n read the last row, unused; pieces past the chunk read its last piece again)
+  constexpr int V16 = HD * ES / 16;            // 16-byte pieces a row
+  constexpr int PIECES = ATT_CHUNK * V16;
+  const char* kb = (const char*)a.cache + ((int64_t)kvh * a.cache_len + row0 + c0) * HD * ES;
+  const char* vb = (const char*)a.cache + ((int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + c0) * HD * ES;
+  const float* qrow = a.q + ((int64_t)b * a.heads + (int64_t)kvh * rep) * HD;
+  for (int i0 = 0; i0 < PIECES; i0 += 4 * nthreads) {
+    uint4 kp[4], vp[4];
+    float4 qp = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int i = 0; i < (int)(sizeof qv / sizeof qv[0]); ++i) {
-    const int d = tid + 64 * ATT_WAVES * i;
-    qv[i] = d < HD ? a.q[((int64_t)b * a.heads + h) * HD + d] : 0.f;
-  }
-  constexpr int EPL = BF ? 8 : 4;  // elements a 16-byte load
-  uint4 kw[HD / EPL];
-  const int64_t kb = ((int64_t)kvh * a.cache_len + row0 + t) * HD;
-#pragma unroll
-  for (int i = 0; i < HD / EPL; ++i) kw[i] = *(const uint4*)((const char*)a.cache + (kb + i * EPL) * (BF ? 2 : 4));
-  // values kept as loaded (bf16 pairs stay packed: half the registers) and widened when used
-  constexpr int VW = BF ? (DL + 1) / 2 : DL;  // 32-bit words a row a lane
-  uint32_t v[64][VW];
-  const int64_t vb = ((int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + w0) * HD + DL * lane;
-#pragma unroll
-  for (int tt = 0; tt < 64; ++tt) {
-    const int64_t at = vb + (int64_t)(tt < n ? tt : 0) * HD;
-    if (BF && DL == 1) v[tt][0] = ((const uint16_t*)a.cache)[at];
-    else if (BF && DL == 2) v[tt][0] = *(const uint32_t*)((const uint16_t*)a.cache + at);
-    else if (BF) { const uint2 w = *(const uint2*)((const uint16_t*)a.cache + at); v[tt][0] = w.x; v[tt][VW - 1] = w.y; }
-    else {
-#pragma unroll
-      for (int i = 0; i < VW; ++i) v[tt][i] = ((const uint32_t*)a.cache)[at + i];
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(i0 + u * nthreads + tid, PIECES - 1);
+      const int r = i / V16, pc = i % V16, rr = r < n ? r : n - 1;
+      kp[u] = *(const uint4*)(kb + (int64_t)rr * HD * ES + 16 * pc);
+      vp[u] = *(const uint4*)(vb + (int64_t)rr * HD * ES + 16 * pc);
     }
-  }
+    if (i0 == 0) qp = *(const float4*)(qrow + 4 * min(tid, rep * HD / 4 - 1));  // (rep HD / 4 <= 16 HD / 4 <= 64 rep)
 #pragma unroll
-  for (int i = 0; i < (int)(sizeof qv / sizeof qv[0]); ++i) {
-    const int d = tid + 64 * ATT_WAVES * i;
-    if (d < HD) qs[d] = qv[i];
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * nthreads + tid;
+      if (i < PIECES) {
+        *(uint4*)(ks + (i / V16) * RW + 16 * (i % V16)) = kp[u];
+        *(uint4*)(vs + (i / V16) * RW + 16 * (i % V16)) = vp[u];
+      }
+    }
+    if (i0 == 0 && tid < rep * HD / 4) *(float4*)(qs + 4 * tid) = qp;
   }
   __syncthreads();
 
-  // the score of the lane's row: the dot with q (read from LDS, the same for every lane)
+  // the lane's row's score: its keys (from LDS) dotted with the head's q (an LDS broadcast)
+  const float* qh = qs + wave * HD;
   float s2[2] = {0.f, 0.f};
+  const char* krow = ks + lane * RW;
 #pragma unroll
-  for (int i = 0; i < HD / EPL; ++i) {
-    const uint32_t w[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+  for (int p = 0; p < V16; ++p) {
+    const uint4 w4 = *(const uint4*)(krow + 16 * p);
+    const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+    const float4 qa = *(const float4*)(qh + p * (16 / ES)), qb = BF ? *(const float4*)(qh + p * 8 + 4) : qa;
+    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (BF) {
-        s2[0] = fmaf(qs[i * EPL + 2 * j], __uint_as_float(w[j] << 16), s2[0]);
-        s2[1] = fmaf(qs[i * EPL + 2 * j + 1], __uint_as_float(w[j] & 0xFFFF0000u), s2[1]);
+        s2[0] = fmaf(qv[2 * j], __uint_as_float(w[j] << 16), s2[0]);
+        s2[1] = fmaf(qv[2 * j + 1], __uint_as_float(w[j] & 0xFFFF0000u), s2[1]);
       } else {
-        s2[j & 1] = fmaf(qs[i * EPL + j], __uint_as_float(w[j]), s2[j & 1]);
+        s2[j & 1] = fmaf(qv[j], __uint_as_float(w[j]), s2[j & 1]);
       }
     }
   }
-  float mx = -INFINITY, sm = 0.f;
-  if (n > 0) {
-    const float sc = valid ? (s2[0] + s2[1]) * a.scale : -INFINITY;
-    mx = wave_max(sc);
-    const float p = valid ? expf(sc - mx) : 0.f;
-    sm = wave_sum(p);
-    ps[wave][lane] = p;
-  }
+  const bool valid = lane < n;
+  const float sc = valid ? (s2[0] + s2[1]) * a.scale : -INFINITY;
+  const float mx = wave_max(sc);
+  const float p = valid ? expf(sc - mx) : 0.f;
+  const float sm = wave_sum(p);
+  ps[lane] = p;
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  // p v (rows past n have p = 0)
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the wave's p visible to all its lanes
+
+  // p v: a lane dimensions DL lane .. DL lane + DL - 1
   float o[DL];
 #pragma unroll
   for (int i = 0; i < DL; ++i) o[i] = 0.f;
-  if (n > 0) {
+#pragma unroll 4
+  for (int t4 = 0; t4 < ATT_CHUNK / 4; ++t4) {
+    const float4 p4 = *(const float4*)(ps + 4 * t4);
+    const float pt[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-    for (int tt = 0; tt < 64; ++tt) {
-      const float p = ps[wave][tt];
+    for (int u = 0; u < 4; ++u) {
+      const char* vr = vs + (4 * t4 + u) * RW + DL * ES * lane;
+      if (BF && DL == 2) {
+        const uint32_t w = *(const uint32_t*)vr;
+        o[0] = fmaf(pt[u], __uint_as_float(w << 16), o[0]);
+        o[1] = fmaf(pt[u], __uint_as_float(w & 0xFFFF0000u), o[1]);
+      } else {
 #pragma unroll
-      for (int i = 0; i < DL; ++i) {
-        const float x = BF ? __uint_as_float(i % 2 ? v[tt][i / 2] & 0xFFFF0000u : v[tt][i / 2] << 16) : __uint_as_float(v[tt][i]);
-        o[i] = fmaf(p, x, o[i]);
+        for (int i = 0; i < DL; ++i) {
+          const float x = BF ? __uint_as_float((uint32_t)((const uint16_t*)vr)[i] << 16) : ((const float*)vr)[i];
+          o[i] = fmaf(pt[u], x, o[i]);
+        }
       }
     }
   }
+  if (nchunks == 1) {  // the row's only chunk: o itself
+    float* ob = a.o + ((int64_t)b * a.heads + h) * HD + DL * lane;
 #pragma unroll
-  for (int i = 0; i < DL; ++i) wo[wave][DL * lane + i] = o[i];
-  if (lane == 0) { wm[wave] = mx; wl[wave] = sm; }
-  __syncthreads();
-
-  // the workgroup's waves combined, a thread a dimension; o itself when the row has one chunk
-  const bool alone = nchunks == 1;
-  for (int d = tid; d < HD; d += 64 * ATT_WAVES) {
-    float big = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < ATT_WAVES; ++w) big = fmaxf(big, wm[w]);
-    float num = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < ATT_WAVES; ++w) {
-      if (wm[w] == -INFINITY) continue;  // a wave past the row's place
-      const float e = expf(wm[w] - big);
-      num = fmaf(e, wo[w][d], num);
-      den = fmaf(e, wl[w], den);
-    }
-    if (alone) {
-      a.o[((int64_t)b * a.heads + h) * HD + d] = num / den;
-    } else {
-      float* pp = a.part + (((int64_t)b * a.heads + h) * a.max_chunks + chunk) * (HD + 2);
-      pp[d] = num;
-      if (d == 0) { pp[HD] = big; pp[HD + 1] = den; }
-    }
+    for (int i = 0; i < DL; ++i) ob[i] = o[i] / sm;
+    return;
   }
+  float* pp = a.part + (((int64_t)b * a.heads + h) * a.max_chunks + chunk) * (HD + 2);
+#pragma unroll
+  for (int i = 0; i < DL; ++i) pp[DL * lane + i] = o[i];
+  if (lane == 0) { pp[HD] = mx; pp[HD + 1] = sm; }
 }
 
-// the chunks of row blockIdx.y, head blockIdx.x combined: a thread a dimension, every chunk's loads in flight
+// The chunks of row blockIdx.y, head blockIdx.x combined, HD threads: thread t holds chunk g0 + t's statistics and
+// dimension t's values of CV chunks at a time. The first round's loads (the row's place, the statistics, the values)
+// go out together; the largest max and the sum of exp-weighted sums are workgroup reductions, each chunk's weight
+// exp(max - the largest) is computed once (by its thread) and shared through LDS. Chunks past the row's (left from
+// other calls) are selected away, never multiplied by 0.
+template <int HD>
+__device__ inline float block_fold(float v, bool is_max, float* red) {
+  v = is_max ? wave_max(v) : wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < HD / 64; ++w) t = is_max ? fmaxf(t, red[w]) : t + red[w];
+  __syncthreads();
+  return t;
+}
+
 template <int HD>
 __global__ __launch_bounds__(HD) void attention_combine(AttArgs a) {
+  constexpr int CV = 32;
+  __shared__ float w_s[HD];
+  __shared__ float red_s[HD / 64];
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  int64_t row0, length;
-  row_range(a, b, row0, length);
-  const int nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);
-  if (nchunks == 1) return;  // the first kernel wrote o
-  const float* pp = a.part + ((int64_t)b * a.heads + h) * a.max_chunks * (HD + 2);
-  float big = -INFINITY, num = 0.f, den = 0.f;
-  for (int c0 = 0; c0 < nchunks; c0 += 16) {  // 16 chunks' loads at once, the running sums rescaled to a new largest
-    float m16[16], l16[16], v16[16];
+  const float* hp = a.part + ((int64_t)b * a.heads + h) * a.max_chunks * (HD + 2);
+  const int last = a.max_chunks - 1;
+  auto values = [&](float (&v)[CV], int c0) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const bool ok = c0 + j < nchunks;
-      const float* q = pp + (int64_t)(ok ? c0 + j : c0) * (HD + 2);
-      m16[j] = ok ? q[HD] : -INFINITY; l16[j] = q[HD + 1]; v16[j] = q[d];
+    for (int j = 0; j < CV; ++j) v[j] = hp[(int64_t)min(c0 + j, last) * (HD + 2) + d];
+  };
+  float big = -INFINITY, den = 0.f, num = 0.f;
+  int nchunks = a.max_chunks;  // (the row's own count, known after the first round)
+  for (int g0 = 0; g0 < nchunks; g0 += HD) {
+    const float* pc = hp + (int64_t)min(g0 + d, last) * (HD + 2);
+    const float mc = pc[HD], lc = pc[HD + 1];
+    float v[CV];
+    values(v, g0);
+    if (g0 == 0) {
+      int64_t row0, length;
+      row_range(a, b, row0, length);
+      nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);
+      if (nchunks == 1) return;  // the first kernel wrote o
     }
-    float top = big;
+    const bool ok = g0 + d < nchunks;
+    const float top = fmaxf(big, block_fold<HD>(ok ? mc : -INFINITY, true, red_s));
+    const float wc = ok ? expf(mc - top) : 0.f;
+    const float f = big == -INFINITY ? 0.f : expf(big - top);
+    den = fmaf(den, f, block_fold<HD>(ok ? wc * lc : 0.f, false, red_s));
+    num *= f;
+    w_s[d] = wc;
+    __syncthreads();
+    const int n = min(HD, nchunks - g0);
+    for (int j0 = 0; j0 < n; j0 += CV) {
+      if (j0 > 0) values(v, g0 + j0);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) top = fmaxf(top, m16[j]);
-    if (big != -INFINITY) { const float f = expf(big - top); num *= f; den *= f; }
+      for (int j = 0; j < CV; ++j) num = j0 + j < n ? fmaf(w_s[j0 + j], v[j], num) : num;
+    }
+    __syncthreads();  // (w_s is rewritten by the next group)
     big = top;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (m16[j] == -INFINITY) continue;
-      const float e = expf(m16[j] - big);
-      num = fmaf(e, v16[j], num);
-      den = fmaf(e, l16[j], den);
-    }
   }
   a.o[((int64_t)b * a.heads + h) * HD + d] = num / den;
 }
 
+// the kernel, allowed its largest LDS (above 64 KiB for fp32 rows of 256 and 16 heads a key head) once
+template <int HD, bool BF>
+static void launch_attention(dim3 grid, dim3 block, size_t lds, hipStream_t s, const AttArgs& a) {
+  static const hipError_t allowed = hipFuncSetAttribute((const void*)attention_kernel<HD, BF>,
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)att_lds(HD, BF ? 2 : 4, ATT_REP));
+  (void)allowed;  // (a refusal shows as the launch's error)
+  hipLaunchKernelGGL((attention_kernel<HD, BF>), grid, block, lds, s, a);
+}
 
 }  // namespace fh
 
@@ -206,6 +245,7 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   if (!q || !cache || !places || !first_row || !o) return fail(FH_EINVAL, "fh_attention_decode: null pointer");
   if (batch < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads)
     return fail(FH_EINVAL, "fh_attention_decode: heads must be a multiple of kv_heads");
+  if (heads / kv_heads > ATT_REP) return fail(FH_EUNSUP, "fh_attention_decode: at most 16 query heads a key head");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(FH_EUNSUP, "fh_attention_decode: head_dim 64, 128 or 256");
   if (cache_dtype != FH_F32 && cache_dtype != FH_BF16) return fail(FH_EUNSUP, "fh_attention_decode: cache is FH_F32 or FH_BF16");
   if (max_context < 1 || max_context > cache_len) return fail(FH_EINVAL, "fh_attention_decode: max_context outside 1..cache_len");
@@ -219,16 +259,18 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   a.max_chunks = (int)((max_context + ATT_CHUNK - 1) / ATT_CHUNK);
   a.o = o;
   a.part = (float*)workspace;
-  dim3 grid(a.max_chunks, heads, batch), block(64 * ATT_WAVES);
-  hipStream_t s = as_stream(stream);
+  const int rep = heads / kv_heads;
+  const dim3 grid(a.max_chunks, kv_heads, batch), block(64 * rep);
   const bool bf = cache_dtype == FH_BF16;
+  const size_t lds = att_lds(head_dim, bf ? 2 : 4, rep);
+  hipStream_t s = as_stream(stream);
   const dim3 cgrid(heads, batch);
   switch (head_dim) {
-    case 64: if (bf) hipLaunchKernelGGL((attention_kernel<64, true>), grid, block, 0, s, a); else hipLaunchKernelGGL((attention_kernel<64, false>), grid, block, 0, s, a);
+    case 64: if (bf) launch_attention<64, true>(grid, block, lds, s, a); else launch_attention<64, false>(grid, block, lds, s, a);
              if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<64>, cgrid, dim3(64), 0, s, a); break;
-    case 128: if (bf) hipLaunchKernelGGL((attention_kernel<128, true>), grid, block, 0, s, a); else hipLaunchKernelGGL((attention_kernel<128, false>), grid, block, 0, s, a);
+    case 128: if (bf) launch_attention<128, true>(grid, block, lds, s, a); else launch_attention<128, false>(grid, block, lds, s, a);
               if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<128>, cgrid, dim3(128), 0, s, a); break;
-    default: if (bf) hipLaunchKernelGGL((attention_kernel<256, true>), grid, block, 0, s, a); else hipLaunchKernelGGL((attention_kernel<256, false>), grid, block, 0, s, a);
+    default: if (bf) launch_attention<256, true>(grid, block, lds, s, a); else launch_attention<256, false>(grid, block, lds, s, a);
              if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<256>, cgrid, dim3(256), 0, s, a); break;
   }
   return check_launch("fh_attention_decode");

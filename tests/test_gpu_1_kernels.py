@@ -195,10 +195,10 @@ def test_epilogues(cuda):
       assert not got[:, mask].any(), "only the rows' places written"
 
 
-@pytest.mark.parametrize("hd,heads,kv", [(64, 9, 3), (128, 32, 8)])
+@pytest.mark.parametrize("hd,heads,kv", [(64, 9, 3), (128, 32, 8), (256, 16, 1)])
 def test_attention_decode(cuda, hd, heads, kv):
-  # rows of a batch at different places (one chunk, several, a chunk's edge), each over its own slot of the cache,
-  # against numpy's softmax(q k^T / sqrt(hd) + mask) v (models/llama.py:141-142)
+  # rows of a batch at different places (one chunk, several, a chunk's edge), each over its own slot of the cache, a
+  # key head shared by 3, 4 and 16 query heads, against numpy's softmax(q k^T / sqrt(hd) + mask) v (models/llama.py:141-142)
   rng = np.random.default_rng(4)
   part, batch = 300, 4
   places = np.array([0, 63, 64, 299], np.int32)
@@ -217,7 +217,7 @@ def test_attention_decode(cuda, hd, heads, kv):
       qq = q[b].reshape(heads, 1, hd).astype(np.float64)
       want = (OL.softmax(qq @ k.swapaxes(-1, -2) / math.sqrt(hd)) @ v).reshape(-1)
       assert np.abs(o[b] - want).max() <= 1e-5 * np.abs(want).max() + 1e-6, (cd, b)
-  # the counters are left at zero: the same call again gives the same result
+  # the same call again gives the same result
   o2 = ops().attention_decode(to_gpu(q), to_gpu(cache, torch.bfloat16), heads, kv, hd, to_gpu(places, torch.int32),
                               to_gpu(first, torch.int32), part, ws).cpu().numpy()
   assert np.array_equal(o, o2)
