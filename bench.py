@@ -304,6 +304,16 @@ def main():
   rates = gemv_rates(dec, stream)
   for k, r in rates.items():
     print(f"# gemv {k:8s} {r['fmt']} {r['K']}x{r['N']}: {r['us']:.2f} us, {r['gbs']:.0f} GB/s ({r['gbs'] * 1e9 / HBM_PEAK:.1%})", file=sys.stderr, flush=True)
+  rates8 = None
+  if args.config == "c3" and B == 1:  # the target's own kernels: the 8B shapes with every matrix bfp8
+    c8, mode8, _ = config("c3-bfp8")
+    dec8 = G.Decoder(c8, G.random_weights(c8, seed=2, device=dev), mode=mode8, kv="bf16", batch=1, context=8)
+    rates8 = gemv_rates(dec8, stream)
+    for k, r8 in rates8.items():
+      print(f"# gemv all-bfp8 {k:8s} {r8['fmt']} {r8['K']}x{r8['N']}: {r8['us']:.2f} us, {r8['gbs']:.0f} GB/s "
+            f"({r8['gbs'] * 1e9 / HBM_PEAK:.1%})", file=sys.stderr, flush=True)
+    del dec8
+    torch.cuda.empty_cache()
   dom = max(rates, key=lambda k: rates[k]["us"] * (c.layers if k != "head" else 1))  # the most time in a step
   r = rates[dom]
   epi = {"qkv": "RMSNorm+RoPE+KV put", "o": "residual", "gate_up": "RMSNorm+SiLU*gate", "down": "residual", "head": "RMSNorm+argmax"}
@@ -340,6 +350,8 @@ def main():
                  "traffic": measured_traffic(dom, args.config, B)},
     "gemv_gbs": {k: round(v["gbs"], 1) for k, v in rates.items()},
     "gemv_us": {k: round(v["us"], 3) for k, v in rates.items()},
+    "gemv_bfp8_8b": None if rates8 is None else {k: {"us": round(v["us"], 3), "gbs": round(v["gbs"], 1),
+                                                     "frac": round(v["gbs"] * 1e9 / HBM_PEAK, 4)} for k, v in rates8.items()},
     "cpu_baseline": cpu,
     "prefill": pre,
     **extra,

@@ -236,7 +236,9 @@ static int dispatch_batch(const MatArgs& a, int batch, int items, int W, hipStre
 }
 
 // The K slices: W waves a workgroup, the least power of 2 giving about 16384 waves in all (64 a CU on 256 CUs, in
-// turns), at most 16 and at most one a group of U loads of 64 rows a lane.
+// turns), at most one a group of U loads of 64 rows a lane, and at most 16 for bfp4 and 8 for bfp8: a bfp8 wave needs
+// ~100 registers at two runs an item, so a 16-wave workgroup fills a CU alone and the grid runs in lock-step rounds
+// (on MI355X: the 8B shapes' bfp8 gate_up 31.7 us at 16, 25.9 at 8; bfp4's down 11.0 at 16, 11.4 at 8).
 struct Plan { int W, rows, P, most, items; };
 static Plan plan(int64_t K, int64_t N, int fmt, int kind, int batch) {
   Plan p;
@@ -246,8 +248,9 @@ static Plan plan(int64_t K, int64_t N, int fmt, int kind, int batch) {
   const int b = batch < p.most ? batch : p.most;
   const int unit = 64 * gemv_group(fmt == FH_BFP4, b, p.P);
   const int64_t units = (K + unit - 1) / unit;
+  const int64_t most = fmt == FH_BFP4 ? 16 : 8;  // (measured: bfp8's 16-wave workgroups run in lock-step rounds)
   int64_t W = 1;
-  while (W < 16 && W * p.items < 16384) W *= 2;
+  while (W < most && W * p.items < 16384) W *= 2;
   while (W > 1 && W > units) W /= 2;
   int64_t rows = (K + W - 1) / W;
   rows = (rows + 63) / 64 * 64;
