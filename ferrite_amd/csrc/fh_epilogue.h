@@ -76,11 +76,14 @@ __host__ __device__ inline int64_t pair_first(int64_t item, int half) { return i
 // A grouped (mixture-of-experts) skinny matmul's extras (fh_skinny.hip): grid.y = expert, its weight `expert_mant` /
 // `expert_exps` bytes on and its outputs `expert_cols` columns on; an expert whose row_scale[.][expert] are all 0 reads
 // nothing; with scale_rows, each row's output is scaled by row_scale[row][expert]; expert e's x starts expert_xcols * e
-// columns into x's rows.
+// columns into x's rows. Or gathered: each expert multiplies only its own rows (below).
 struct SkinnyMoe {
   int64_t expert_mant, expert_exps, expert_cols, expert_xcols;
   const float* row_scale; int experts;
   int scale_rows;
+  // gathered (counts set): expert e takes counts[e] rows (at most M); its x row r is row x_rows[e M + r] of x (row
+  // e M + r where x_rows is null), its output row r is y's row e M + r, and (scale_rows) its scale row_w[e M + r]
+  const int32_t* counts; const int32_t* x_rows; const float* row_w;
 };
 
 // x @ W for up to 64 rows a pass on the matrix cores (fh_skinny.hip); a's epilogue already checked

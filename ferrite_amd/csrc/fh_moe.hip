@@ -7,12 +7,14 @@
 // taken at the k, as norm_topk says), written as ids and weights and as a dense [rows][experts] matrix of weights (0
 // where a row did not pick an expert).
 //
-// fh_moe_experts: ferrite's dense path for a decode step's few tokens (Tensor.touched, chip_experts: every expert some
-// row picked takes every row, weighted by each row's weight, 0 where it did not pick it; llama.py:302-321): the skinny
-// matrix-core kernel over (32 columns, expert) for gate_up with the SiLU·gate epilogue scaled by the row's weight into
-// a [rows][experts * ffn] bf16 workspace, then for down into [rows][experts * dim] fp32, and a last kernel sums the
-// experts in expert order (no atomics: the result does not depend on timing) onto the residual. An expert no row
-// picked reads no weight and leaves zeros.
+// fh_moe_experts: the experts of a decode step's few tokens (ferrite's dense path, Tensor.touched / chip_experts,
+// llama.py:302-321, computes every picked expert for every row, weighted 0 where a row did not pick it; the sum is the
+// same). Here each expert multiplies only its own rows: a first kernel writes the rows (normed when norm_w is given)
+// as bf16 once and, from dense, each expert's list of the rows that picked it (in row order) with their weights;
+// the skinny matrix-core kernel over (32 columns, expert) then takes gate_up for the expert's rows through the list,
+// with the SiLU·gate epilogue scaled by the row's weight, into the expert's own bf16 rows, and down on those into the
+// expert's own fp32 rows; a last kernel adds each row's experts in expert order (no atomics: the result does not
+// depend on timing) onto the residual. An expert no row picked reads no weight.
 #include <math.h>
 #include "fh_epilogue.h"
 
@@ -104,24 +106,81 @@ __global__ __launch_bounds__(RT_THREADS) void route_kernel(const float* x, int64
   }
 }
 
-// y[row] = residual[row] + the experts' outputs summed in expert order, and y's sums of squares by 16 columns
-__global__ __launch_bounds__(256) void moe_sum_kernel(const float* parts, int experts, int dim, const float* residual,
-                                                      float* y, float* ssq_out) {
-  const int64_t row = blockIdx.x;
-  for (int n0 = 0; n0 < dim; n0 += 256) {
-    const int n = n0 + threadIdx.x;
-    float v = 0.f;
-    if (n < dim) {
-      v = residual ? residual[row * dim + n] : 0.f;
-      for (int e = 0; e < experts; ++e) v += parts[(row * experts + e) * dim + n];
-      y[row * dim + n] = v;
+// Blocks 0 .. n-1: row r of x as bf16 into xn (times 1 / rms from the sums of squares by runs of 16 and the RMSNorm
+// weight, when norm_w is given). Block n: each expert's rows (thread e: the rows whose dense weight for e is not 0,
+// in row order), their weights, the counts, and each row's slot in each expert's list (-1 where it did not pick it).
+__global__ __launch_bounds__(256) void moe_prep_kernel(const float* x, int64_t ldx, int n, int dim, const float* norm_w,
+                                                       const float* ssq_in, float eps, int centered, const float* dense,
+                                                       int E, uint16_t* xn, int32_t* counts, int32_t* rows_of,
+                                                       float* row_w, int32_t* slot) {
+  __shared__ float red_s[4];
+  const int r = blockIdx.x, t = threadIdx.x;
+  if (r == n) {
+    for (int e = t; e < E; e += 256) {
+      int c = 0;
+      for (int i = 0; i < n; ++i) {
+        const float w = dense[(int64_t)i * E + e];
+        if (w != 0.f) { rows_of[e * n + c] = i; row_w[e * n + c] = w; slot[i * E + e] = c; ++c; }
+        else slot[i * E + e] = -1;
+      }
+      counts[e] = c;
     }
-    if (ssq_out) {  // (dim is a multiple of 64: a run of 16 is 16 neighbouring lanes, all in range)
-      float s = v * v;
-      s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
-      if (n < dim && (n & 15) == 0) ssq_out[row * (dim / 16) + n / 16] = s;
-    }
+    return;
   }
+  float rs = 1.f;
+  if (norm_w) {
+    const int parts = dim / 16;
+    float s = 0.f;
+    for (int i = t; i < parts; i += 256) s += ssq_in[(int64_t)r * parts + i];
+    s = wave_sum(s);
+    if ((t & 63) == 0) red_s[t >> 6] = s;
+    __syncthreads();
+    rs = 1.0f / sqrtf((red_s[0] + red_s[1] + red_s[2] + red_s[3]) / (float)dim + eps);
+  }
+  for (int i = t; i < dim; i += 256) {
+    float v = x[(int64_t)r * ldx + i];
+    if (norm_w) v *= rs * (centered ? norm_w[i] + 1.f : norm_w[i]);
+    xn[(int64_t)r * dim + i] = (uint16_t)bf16_rne_f(v);
+  }
+}
+
+// y[row] = residual[row] + the row's experts' outputs (parts: each expert's own rows) in expert order, and y's sums of
+// squares by 16 columns; a workgroup 256 columns of a row
+__global__ __launch_bounds__(256) void moe_sum_kernel(const float* parts, const int32_t* slot, int experts, int n, int dim,
+                                                      const float* residual, float* y, float* ssq_out) {
+  const int64_t row = blockIdx.x;
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  float v = 0.f;
+  if (c < dim) {
+    v = residual ? residual[row * dim + c] : 0.f;
+    for (int e = 0; e < experts; ++e) {
+      const int sl = slot[row * experts + e];
+      if (sl >= 0) v += parts[((int64_t)e * n + sl) * dim + c];
+    }
+    y[row * dim + c] = v;
+  }
+  if (ssq_out) {  // (dim is a multiple of 64: a run of 16 is 16 neighbouring lanes, all in range)
+    float s = v * v;
+    s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
+    if (c < dim && (c & 15) == 0) ssq_out[row * (dim / 16) + c / 16] = s;
+  }
+}
+
+// A pass's workspace (n rows, E experts): counts [E], rows_of [E][n], row_w [E][n], slot [n][E], xn [n][dim] bf16,
+// g [E][n][ffn] bf16, parts [E][n][dim] fp32, each region 256-byte aligned
+struct MoeSpace { size_t counts, rows_of, row_w, slot, xn, g, parts, total; };
+static MoeSpace moe_space(int64_t n, int64_t E, int64_t ffn, int64_t dim) {
+  auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+  MoeSpace m;
+  m.counts = 0;
+  m.rows_of = m.counts + up(E * 4);
+  m.row_w = m.rows_of + up(E * n * 4);
+  m.slot = m.row_w + up(E * n * 4);
+  m.xn = m.slot + up(n * E * 4);
+  m.g = m.xn + up(n * dim * 2);
+  m.parts = m.g + up(E * n * ffn * 2);
+  m.total = m.parts + up(E * n * dim * 4);
+  return m;
 }
 
 }  // namespace fh
@@ -147,8 +206,9 @@ extern "C" int fh_moe_route(const float* x, int64_t ldx, int rows, int64_t dim, 
 }
 
 extern "C" size_t fh_moe_workspace_bytes(int rows, int experts, int64_t ffn, int64_t dim) {
-  const int64_t r = rows < 64 ? rows : 64;  // a pass: its gate_up outputs (bf16) and its experts' down outputs (fp32)
-  return (size_t)(r > 0 ? r : 0) * experts * (ffn * 2 + dim * 4);
+  const int64_t r = rows < 64 ? rows : 64;  // a pass of up to 64 rows
+  if (r < 1 || experts < 1 || ffn < 1 || dim < 1) return 0;
+  return moe_space(r, experts, ffn, dim).total;
 }
 
 extern "C" int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim, const float* norm_w, const float* ssq_in,
@@ -171,37 +231,46 @@ extern "C" int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim
   if (int rc = fh_bfp_bytes(ffn, dim, down_fmt, FH_AXIS_N, &dmb, &deb)) return rc;
   for (int r0 = 0; r0 < rows; r0 += 64) {  // 64 rows a pass
     const int n = rows - r0 < 64 ? rows - r0 : 64;
-    uint16_t* g = (uint16_t*)workspace;                                   // [n][experts * ffn] bf16
-    float* parts = (float*)((char*)workspace + (size_t)n * experts * ffn * 2);  // [n][experts * dim]
-    // gate_up of every picked expert: silu(gate) * up * the row's weight
+    const MoeSpace m = moe_space(n, experts, ffn, dim);
+    char* w = (char*)workspace;
+    int32_t* counts = (int32_t*)(w + m.counts);
+    int32_t* rows_of = (int32_t*)(w + m.rows_of);
+    float* row_w = (float*)(w + m.row_w);
+    int32_t* slot = (int32_t*)(w + m.slot);
+    uint16_t* xn = (uint16_t*)(w + m.xn);
+    uint16_t* g = (uint16_t*)(w + m.g);          // [experts][n][ffn]
+    float* parts = (float*)(w + m.parts);        // [experts][n][dim]
+    hipLaunchKernelGGL(moe_prep_kernel, dim3(n + 1), dim3(256), 0, s, x + (int64_t)r0 * ldx, ldx, n, (int)dim, norm_w,
+                       ssq_in ? ssq_in + (int64_t)r0 * (dim / 16) : nullptr, eps, centered, dense + (int64_t)r0 * experts,
+                       experts, xn, counts, rows_of, row_w, slot);
+    // gate_up of each expert on its rows: silu(gate) * up * the row's weight
     MatArgs a = {};
     fh_epilogue ep = {};
-    ep.kind = FH_EP_SILU_GATE; ep.split = (int)ffn; ep.norm_w = norm_w; ep.ssq_in = ssq_in ? ssq_in + (int64_t)r0 * (dim / 16) : nullptr;
-    ep.eps = eps; ep.centered = centered;
-    a.x = x + (int64_t)r0 * ldx; a.ldx = ldx; a.x_bf16 = 0;
+    ep.kind = FH_EP_SILU_GATE; ep.split = (int)ffn;
+    a.x = xn; a.ldx = dim; a.x_bf16 = 1;
     a.mant = (const uint8_t*)gu_mant; a.exps = gu_exps; a.K = dim; a.N = gu_n; a.M = n;
     a.y = g; a.y_bf16 = 1;
     if (int rc = epilogue_args("fh_moe_experts", &ep, dim, gu_n, FH_BF16, ffn, a)) return rc;
-    a.ldy = (int64_t)experts * ffn;
+    a.ldy = ffn;
     SkinnyMoe moe = {};
-    moe.expert_mant = (int64_t)mb; moe.expert_exps = (int64_t)eb; moe.expert_cols = ffn;
-    moe.row_scale = dense + (int64_t)r0 * experts; moe.experts = experts; moe.scale_rows = 1;
+    moe.expert_mant = (int64_t)mb; moe.expert_exps = (int64_t)eb; moe.experts = experts; moe.scale_rows = 1;
+    moe.counts = counts; moe.x_rows = rows_of; moe.row_w = row_w;
     if (int rc = skinny_matmul(a, moe, gu_fmt, experts, s)) return rc;
-    // down, each picked expert's own outputs
+    // down, each expert on its own rows of g
     MatArgs d = {};
     fh_epilogue de = {};
     de.kind = FH_EP_STORE;
-    d.x = g; d.ldx = (int64_t)experts * ffn; d.x_bf16 = 1;
+    d.x = g; d.ldx = ffn; d.x_bf16 = 1;
     d.mant = (const uint8_t*)down_mant; d.exps = down_exps; d.K = ffn; d.N = dim; d.M = n;
     d.y = parts; d.y_bf16 = 0;
     if (int rc = epilogue_args("fh_moe_experts", &de, ffn, dim, FH_F32, dim, d)) return rc;
-    d.ldy = (int64_t)experts * dim;
+    d.ldy = dim;
     SkinnyMoe dm = {};
-    dm.expert_mant = (int64_t)dmb; dm.expert_exps = (int64_t)deb; dm.expert_cols = dim; dm.expert_xcols = ffn;
-    dm.row_scale = dense + (int64_t)r0 * experts; dm.experts = experts; dm.scale_rows = 0;
+    dm.expert_mant = (int64_t)dmb; dm.expert_exps = (int64_t)deb; dm.experts = experts; dm.scale_rows = 0;
+    dm.counts = counts;
     if (int rc = skinny_matmul(d, dm, down_fmt, experts, s)) return rc;
-    hipLaunchKernelGGL(moe_sum_kernel, dim3(n), dim3(256), 0, s, parts, experts, (int)dim,
-                       residual ? residual + (int64_t)r0 * dim : nullptr, y + (int64_t)r0 * dim,
+    hipLaunchKernelGGL(moe_sum_kernel, dim3(n, (unsigned)((dim + 255) / 256)), dim3(256), 0, s, parts, slot, experts, n,
+                       (int)dim, residual ? residual + (int64_t)r0 * dim : nullptr, y + (int64_t)r0 * dim,
                        ssq_out ? ssq_out + (int64_t)r0 * (dim / 16) : nullptr);
     if (int rc = check_launch("fh_moe_experts")) return rc;
   }

@@ -15,7 +15,9 @@
 // For a mixture of experts the grid's second dimension is the expert: the weight is the expert's (`expert_mant` /
 // `expert_exps` bytes apart), its outputs go `expert_cols` columns further on (and its x `expert_xcols`), and
 // (scale_rows) each row's output is scaled by that row's weight for the expert (0 where the row did not pick it); an
-// expert no row picked reads nothing.
+// expert no row picked reads nothing. Gathered (SkinnyMoe::counts), an expert takes only the rows that picked it,
+// through a list of their indices, and writes its outputs to rows of its own: x's traffic is each expert's rows, not
+// every row once an item.
 #include "fh_epilogue.h"
 
 namespace fh {
@@ -49,14 +51,22 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
 
   const int item = blockIdx.x, e = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), W = blockDim.x >> 6;
-  const int M = (int)a.M, K = (int)a.K;
+  const bool gathered = moe.counts != nullptr;
+  const int M = gathered ? min(moe.counts[e], (int)a.M) : (int)a.M, K = (int)a.K;
+  // a row's place in x and in y (gathered: the expert's own rows)
+  auto xrow = [&](int r) -> int64_t {
+    return gathered ? (moe.x_rows ? moe.x_rows[(int64_t)e * a.M + r] : (int64_t)e * a.M + r) : r;
+  };
+  const int64_t yrow0 = gathered ? (int64_t)e * a.M : 0;
 
   // the rows' weights for this expert; an expert no row picked writes its zeros and reads nothing
-  if (t == 0) any_s = moe.row_scale ? 0 : 1;
+  if (t == 0) any_s = gathered ? M > 0 : (moe.row_scale ? 0 : 1);
   __syncthreads();
   if (t < 16 * MB) {
     float sc = 1.f;
-    if (moe.row_scale) {
+    if (gathered) {
+      if (moe.scale_rows) sc = t < M ? moe.row_w[(int64_t)e * a.M + t] : 0.f;
+    } else if (moe.row_scale) {
       const float r = t < M ? moe.row_scale[(int64_t)t * moe.experts + e] : 0.f;
       if (r != 0.f) any_s = 1;
       if (moe.scale_rows) sc = r;
@@ -67,7 +77,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   for (int row = wave; row < 16 * MB; row += W) {
     float r = 1.f;
     if (NORM && row < M) {
-      const float* q = a.ssq_in + (int64_t)row * a.ssq_parts;
+      const float* q = a.ssq_in + xrow(row) * a.ssq_parts;
       float s = 0.f;
       for (int i = lane; i < a.ssq_parts; i += 64) s += q[i];
       s = wave_sum(s);
@@ -106,7 +116,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
     const char* xp[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b)
-      xp[b] = (const char*)a.x + ((int64_t)min(16 * b + (lane & 15), M - 1) * a.ldx + (int64_t)e * moe.expert_xcols + 8 * (lane >> 4)) * (XBF16 ? 2 : 4);
+      xp[b] = (const char*)a.x + (xrow(min(16 * b + (lane & 15), M - 1)) * a.ldx + (int64_t)e * moe.expert_xcols + 8 * (lane >> 4)) * (XBF16 ? 2 : 4);
     const int last = r1 - SK_BK;  // (r1 - r0 is a multiple of 64: K is)
     // the transposed reads' addresses in the tile: 16-lane group g reads k 8 (g / 2)... of the 32-k block; in the
     // group, lane 4 m + q points at row m, columns 4 q .. 4 q + 3 of the run
@@ -243,7 +253,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       const int64_t run = nb[c >> 4];
       const bool ok = row < M && (c < 16 || run1_ok);
       const int64_t col = run * 16 + j;
-      const int64_t at = (int64_t)row * a.ldy + col + col_off;
+      const int64_t at = (yrow0 + row) * a.ldy + col + col_off;
       float v = fin[row * PLD + c] * scale_s[row];
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
       if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, row, col);
@@ -251,7 +261,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;
         s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
-        if (ok && j == 0) a.ssq_out[(int64_t)row * (a.N / 16) + run] = s;
+        if (ok && j == 0) a.ssq_out[(yrow0 + row) * (a.N / 16) + run] = s;
       }
       if (kind == FH_EP_STORE && a.argmax_parts) {
         float bv = v;
@@ -262,7 +272,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
           const int oc = __shfl_xor(bc, s, 64);
           if (ov > bv || (ov == bv && oc < bc)) { bv = ov; bc = oc; }
         }
-        if (ok && j == 0) a.argmax_parts[(int64_t)row * (a.N / 16) + run] = make_int2(__float_as_int(bv), bc);
+        if (ok && j == 0) a.argmax_parts[(yrow0 + row) * (a.N / 16) + run] = make_int2(__float_as_int(bv), bc);
       }
     }
   } else {  // the pair: columns 0..15 the first run (gate, or a head's first half), 16..31 its partner
@@ -272,7 +282,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       float x0 = fin[row * PLD + j], x1 = fin[row * PLD + 16 + j];
       const int64_t c0 = nb[0] * 16 + j;
       if (kind == FH_EP_SILU_GATE) {
-        store_out(a.y, a.y_bf16, (int64_t)row * a.ldy + c0 + col_off, silu(x0) * x1 * scale_s[row]);
+        store_out(a.y, a.y_bf16, (yrow0 + row) * a.ldy + c0 + col_off, silu(x0) * x1 * scale_s[row]);
       } else {  // FH_EP_ROPE_KV
         const int hd = a.head_dim;
         const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
