@@ -29,7 +29,8 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
 
 __device__ inline uint32_t pack_bf16_exact(float lo, float hi) {  // both exact in bf16: the high halves
-  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+  // (the high halves of two floats whose low halves are 0: one byte permute, v_perm_b32)
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 __device__ inline uint32_t pack_bf16_rne(float lo, float hi) { return bf16_rne_f(lo) | (bf16_rne_f(hi) << 16); }
 

@@ -2,7 +2,7 @@
 // experts' SwiGLUs weighted and summed.
 //
 // fh_moe_route: a workgroup a token row: RMSNorm of the row (if norm_w), the router's logits (fp32 sums of the row
-// times the router's bf16 or fp32 columns, the threads splitting the row), the k largest (the first of equals first,
+// times the router's bf16 or fp32 columns, each thread a share of the router's rows), the k largest (the first of equals first,
 // as numpy's stable argsort orders them, llama.py:27), and their weights (a softmax over the k, or the softmax over all
 // taken at the k, as norm_topk says), written as ids and weights and as a dense [rows][experts] matrix of weights (0
 // where a row did not pick an expert).
@@ -26,7 +26,7 @@ template <bool RBF16>
 __global__ __launch_bounds__(RT_THREADS) void route_kernel(const float* x, int64_t ldx, int dim, const float* norm_w,
                                                            float eps, int centered, const void* router, int E, int k,
                                                            int norm_topk, int32_t* ids, float* wts, float* dense) {
-  extern __shared__ float rt_smem[];   // [dim] the normed row, then [parts][E] partial logits
+  extern __shared__ float rt_smem[];   // [dim] the normed row
   __shared__ float logit_s[256];
   __shared__ float red_s[RT_THREADS / 64];
   const int64_t row = blockIdx.x;
@@ -50,26 +50,49 @@ __global__ __launch_bounds__(RT_THREADS) void route_kernel(const float* x, int64
     h[i] = norm_w ? xr[i] * rs * g : xr[i];
   }
   __syncthreads();
-  // logits: thread t takes expert t % E over part t / E of the row
-  const int parts = RT_THREADS / E;
-  float* partial = h + dim;
-  if (t < parts * E) {
-    const int e = t % E, p = t / E;
-    const int per = (dim + parts - 1) / parts, k0 = p * per, k1 = min(dim, k0 + per);
-    float s = 0.f;
-    for (int i = k0; i < k1; ++i) {
-      const float w = RBF16 ? bf16_to_f(((const uint16_t*)router)[(int64_t)i * E + e]) : ((const float*)router)[(int64_t)i * E + e];
-      s += h[i] * w;
+  // logits, 8 experts at a time: thread t takes the router's rows t, t + 256, .. (a row's 8 values one 16-byte load
+  // where the layout allows), then the workgroup sums each expert's partials in a fixed order
+  constexpr int EC = 8;
+  __shared__ float part8[RT_THREADS / 64][EC];
+  const bool wide = RBF16 && E % 8 == 0;
+  for (int e0 = 0; e0 < E; e0 += EC) {
+    float acc[EC];
+#pragma unroll
+    for (int j = 0; j < EC; ++j) acc[j] = 0.f;
+#pragma unroll 4
+    for (int i = t; i < dim; i += RT_THREADS) {
+      const float hv = h[i];
+      if (wide) {
+        const uint4 w = *(const uint4*)((const uint16_t*)router + (int64_t)i * E + e0);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[2 * j] = fmaf(hv, __uint_as_float(ww[j] << 16), acc[2 * j]);
+          acc[2 * j + 1] = fmaf(hv, __uint_as_float(ww[j] & 0xFFFF0000u), acc[2 * j + 1]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < EC; ++j) {
+          const int e = min(e0 + j, E - 1);
+          const float w = RBF16 ? bf16_to_f(((const uint16_t*)router)[(int64_t)i * E + e]) : ((const float*)router)[(int64_t)i * E + e];
+          acc[j] = fmaf(hv, w, acc[j]);
+        }
+      }
     }
-    partial[p * E + e] = s;
+#pragma unroll
+    for (int j = 0; j < EC; ++j) {
+      const float v = wave_sum(acc[j]);
+      if ((t & 63) == 0) part8[t >> 6][j] = v;
+    }
+    __syncthreads();
+    if (t < EC && e0 + t < E) {
+      float v = part8[0][t];
+#pragma unroll
+      for (int w = 1; w < RT_THREADS / 64; ++w) v += part8[w][t];
+      logit_s[e0 + t] = v;
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (t < E) {
-    float s = 0.f;
-    for (int p = 0; p < parts; ++p) s += partial[p * E + t];
-    logit_s[t] = s;
-  }
-  __syncthreads();
   if (t == 0) {
     // softmax over all first when the k are not renormalised (their probabilities among all)
     if (!norm_topk) {
@@ -194,8 +217,7 @@ extern "C" int fh_moe_route(const float* x, int64_t ldx, int rows, int64_t dim, 
   if (rows < 1 || dim < 1 || ldx < dim) return fail(FH_EINVAL, "fh_moe_route: need rows, dim >= 1, ldx >= dim");
   if (experts < 1 || experts > 256 || k < 1 || k > 16 || k > experts) return fail(FH_EUNSUP, "fh_moe_route: 1 <= k <= 16, k <= experts <= 256");
   if (router_dtype != FH_F32 && router_dtype != FH_BF16) return fail(FH_EINVAL, "fh_moe_route: router is FH_F32 or FH_BF16");
-  const int parts = RT_THREADS / experts;
-  const size_t lds = ((size_t)dim + (size_t)parts * experts) * sizeof(float);
+  const size_t lds = (size_t)dim * sizeof(float);
   if (lds > 120 * 1024) return fail(FH_EUNSUP, "fh_moe_route: row too long");
   hipStream_t s = as_stream(stream);
   if (router_dtype == FH_BF16)

@@ -33,7 +33,8 @@ constexpr int SK_TILE = SK_BK * SK_RS; // the wave's tile, bf16 values: 5,120 by
 constexpr int SK_RING = 4;             // steps of weight loads in flight
 
 __device__ inline uint32_t sk_pack_exact(float lo, float hi) {
-  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+  // (the high halves of two floats whose low halves are 0: one byte permute, v_perm_b32)
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
 // threads a workgroup at most: fewer where a lane holds more, so that registers do not spill
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       __builtin_amdgcn_sched_barrier(0);
       const int k = min(k0, last) + lane;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) { w[j] = *(const Row*)(mrun[j] + (int64_t)k * RB); ex[j] = erun[j][k]; }
+      for (int j = 0; j < 2; ++j) { w[j] = *(const Row*)(mrun[j] + (uint32_t)k * RB); ex[j] = erun[j][(uint32_t)k]; }
       __builtin_amdgcn_sched_barrier(0);
     };
     uint4 xv[2][MB][2][XW];  // [set][block][k32 half][16 bytes]
