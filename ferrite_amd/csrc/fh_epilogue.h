@@ -18,7 +18,7 @@ struct MatArgs {
   // epilogue
   int kind;
   void* y; int64_t ldy; int y_bf16;
-  const float* residual; float* ssq_out;
+  const float* residual; float* ssq_out; uint16_t* copy_bf16; const float* copy_w;
   int split;
   int heads, kv_heads, head_dim;
   const float* cos_tab; const float* sin_tab; const int32_t* places; const int32_t* cache_rows;
@@ -97,8 +97,10 @@ inline int epilogue_args(const char* who, const fh_epilogue* ep, int64_t K, int6
   a.kind = ep ? ep->kind : FH_EP_STORE;
   a.P = 1; a.pair_half = 1;
   int64_t out_cols = N;
+  if (ep && ep->copy_bf16 && ep->kind != FH_EP_RESIDUAL) return bad(FH_EINVAL, "copy_bf16 is FH_EP_RESIDUAL's");
+  if (ep && ep->copy_w && !ep->copy_bf16) return bad(FH_EINVAL, "copy_w scales copy_bf16");
   if (ep) {
-    if (ep->norm_w) {
+    if (ep->norm_w || ep->ssq_in) {  // (ssq_in alone: rows that already hold x * w, scaled by 1/rms only)
       if (!ep->ssq_in || K % 16) return bad(FH_EINVAL, "RMSNorm prologue needs ssq_in and K a multiple of 16");
       a.norm_w = ep->norm_w; a.ssq_in = ep->ssq_in; a.ssq_parts = (int)(K / 16); a.eps = ep->eps; a.centered = ep->centered;
     }
@@ -106,7 +108,7 @@ inline int epilogue_args(const char* who, const fh_epilogue* ep, int64_t K, int6
       case FH_EP_STORE: a.argmax_parts = (int2*)ep->argmax_parts; break;
       case FH_EP_RESIDUAL:
         if (!ep->residual) return bad(FH_EINVAL, "FH_EP_RESIDUAL needs residual");
-        a.residual = ep->residual; a.ssq_out = ep->ssq_out;
+        a.residual = ep->residual; a.ssq_out = ep->ssq_out; a.copy_bf16 = (uint16_t*)ep->copy_bf16; a.copy_w = ep->copy_w;
         if (y_dtype != FH_F32) return bad(FH_EUNSUP, "FH_EP_RESIDUAL writes fp32");
         break;
       case FH_EP_SILU_GATE:

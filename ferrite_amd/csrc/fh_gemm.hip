@@ -162,7 +162,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
   load(GM_BK, x1, w1, e1);
 
   // each row's 1 / rms from the sums of squares its maker left by runs of 16 (two threads a row)
-  if (NORM) {
+  if (a.ssq_in) {  // (NORM, or rows that already hold x * w)
     float s = 0.f;
     if (xok) {
       const float* q = a.ssq_in + xrow * a.ssq_parts;
@@ -239,6 +239,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
       if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, m, col);
       if (ok) store_out(a.y, a.y_bf16, at, v);
+      if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) a.copy_bf16[m * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;
         s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);

@@ -56,7 +56,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
 #pragma unroll
       for (int i = 0; i < PRE; ++i) {
         const int at = lane + 64 * i;
-        ssq_pre[b][i] = (NORM && a.ssq_parts <= 64 * PRE && at < a.ssq_parts) ? a.ssq_in[(int64_t)b * a.ssq_parts + at] : 0.f;
+        ssq_pre[b][i] = (a.ssq_in && a.ssq_parts <= 64 * PRE && at < a.ssq_parts) ? a.ssq_in[(int64_t)b * a.ssq_parts + at] : 0.f;
       }
       place_pre[b] = a.places ? a.places[b] : 0;
     }
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
 #pragma unroll
   for (int b = 0; b < B; ++b) {
     rs[b] = 1.f;
-    if (NORM) {
+    if (a.ssq_in) {  // (NORM, or rows that already hold x * w)
       float s = 0.f;
       if (a.ssq_parts <= 64 * PRE) {
 #pragma unroll
@@ -147,10 +147,11 @@ __global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
     for (int i = lane; i < V; i += 64) {  // (V is a multiple of 16: a run's 16 values are 16 neighbouring lanes)
       const int b = i / (P * 16), p = (i / 16) % P, j = i % 16;
       const int64_t col = nb[p] * 16 + j, at = b * a.ldy + col;
-      float v = fin[i] * (NORM ? rs[b] : 1.f);
+      float v = fin[i] * rs[b];
       if (kind == FH_EP_RESIDUAL) v += a.residual[at];
       if (kind == FH_EP_PROGRAM) v = prog_eval(a.prog, v, 0, b, col);
       store_out(a.y, a.y_bf16, at, v);
+      if (kind == FH_EP_RESIDUAL && a.copy_bf16) a.copy_bf16[b * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;
         s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
   } else if (P == 2 && kind == FH_EP_SILU_GATE) {
     for (int i = lane; i < B * 16; i += 64) {
       const int b = i / 16, j = i % 16;
-      const float r = NORM ? rs[b] : 1.f;
+      const float r = rs[b];
       const float gv = fin[(b * P) * 16 + j] * r, uv = fin[(b * P + 1) * 16 + j] * r;
       store_out(a.y, a.y_bf16, b * a.ldy + nb[0] * 16 + j, silu(gv) * uv);
     }
@@ -181,7 +182,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
       const int b = i / 16, j = i % 16;
       const int64_t c0 = nb[0] * 16 + j;            // in the first half of its head
       const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
-      const float r = NORM ? rs[b] : 1.f;
+      const float r = rs[b];
       float x0 = fin[(b * P) * 16 + j] * r, x1 = fin[(b * P + 1) * 16 + j] * r;
       int place = place_pre[0];
 #pragma unroll
@@ -289,6 +290,7 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
     c.y = (char*)y + (size_t)b0 * ldy * (a.y_bf16 ? 2 : 4);
     if (c.ssq_in) c.ssq_in += (int64_t)b0 * c.ssq_parts;
     if (c.residual) c.residual += (int64_t)b0 * ldy;
+    if (c.copy_bf16) c.copy_bf16 += (int64_t)b0 * N;
     if (c.ssq_out) c.ssq_out += (int64_t)b0 * (N / 16);
     if (c.places) { c.places += b0; c.cache_rows += b0; }
     if (c.argmax_parts) c.argmax_parts += (int64_t)b0 * (N / 16);

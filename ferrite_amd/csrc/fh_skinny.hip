@@ -77,7 +77,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   // each row's 1 / rms from the sums of squares its maker left by runs of 16: wave w the rows w, w + W, ..
   for (int row = wave; row < 16 * MB; row += W) {
     float r = 1.f;
-    if (NORM && row < M) {
+    if (a.ssq_in && row < M) {  // (NORM, or rows that already hold x * w)
       const float* q = a.ssq_in + xrow(row) * a.ssq_parts;
       float s = 0.f;
       for (int i = lane; i < a.ssq_parts; i += 64) s += q[i];
@@ -259,6 +259,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
       if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, row, col);
       if (ok) store_out(a.y, a.y_bf16, at, v);
+      if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) a.copy_bf16[(yrow0 + row) * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;
         s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
@@ -348,6 +349,7 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
     a.y = (char*)a0.y + m0 * a0.ldy * (a0.y_bf16 ? 2 : 4);
     if (a.ssq_in) a.ssq_in += m0 * a.ssq_parts;
     if (a.residual) a.residual += m0 * a0.ldy;
+    if (a.copy_bf16) a.copy_bf16 += m0 * a0.N;
     if (a.ssq_out) a.ssq_out += m0 * (a0.N / 16);
     if (a.places) { a.places += m0; a.cache_rows += m0; }
     if (a.argmax_parts) a.argmax_parts += m0 * (a0.N / 16);

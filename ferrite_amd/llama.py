@@ -136,7 +136,7 @@ class Decoder:
     self.x, self.ssq = z(B, c.dim), z(B, c.dim // 16)
     self.q, self.att = z(B, c.heads * hd), z(B, c.heads * hd)
     self.h = z(B, c.ffn)
-    self.xn = torch.zeros(B, c.dim, dtype=torch.bfloat16, device=self.device)   # the matrix cores' normed rows
+    self.xn = torch.zeros(B, c.dim, dtype=torch.bfloat16, device=self.device)   # the matrix cores' bf16 rows (each residual epilogue's copy)
     self.hb = torch.zeros(B, c.ffn, dtype=torch.bfloat16, device=self.device)
     self.logits = z(B, c.vocab)
     self.picks = torch.zeros(B, dtype=torch.int32, device=self.device)
@@ -179,25 +179,40 @@ class Decoder:
     ops.gemv(self.x, self.head, ep, out=self.logits)
     ops.argmax_parts(self.parts, self.picks)
 
+  def _norm_weights(self):
+    """Each RMSNorm's multiplier (its weight, + 1 where centered) in the order a step meets them: block l's norm1,
+    norm2, ..., then the final norm."""
+    if getattr(self, "_nw", None) is None:
+      c = self.c
+      ws = [w for L in self.layers for w in (L.norm1, L.norm2)] + [self.norm]
+      self._nw = [w + 1 if c.centered else w for w in ws]
+    return self._nw
+
   def _step_rows(self):
-    """A step of many rows on the matrix cores: each RMSNorm its own kernel writing bf16 rows (the skinny kernel's
-    fast input), SwiGLU's output bf16, the residual stream fp32."""
+    """A step of many rows on the matrix cores. The residual stream stays fp32; each residual epilogue also writes
+    its rows times the next RMSNorm's weight in bf16 (copy_bf16, copy_w) with their sums of squares, and the next
+    matmul takes those rows scaled by 1/rms (ssq_in alone): the products are its RMSNorm prologue's, bf16(x w), with
+    no normalising pass (the first block's norm a kernel of its own). SwiGLU's output bf16."""
     c, B, hd = self.c, self.batch, self.hd
+    nw = self._norm_weights()
     ops.embed_rows(self.embed, self.ids, self.x, self.ssq)
     cache_dtype = lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"]
+    rs = dict(ssq_in=self.ssq, eps=c.eps)  # rows that hold x w: 1/rms only
     for l, L in enumerate(self.layers):
-      ops.rms_rows(self.x, L.norm1, c.eps, c.centered, out=self.xn)
-      ep = ops.epilogue(lib.EP_ROPE_KV, heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
-                        places=self.places, cache_rows=self.rows, cache=self.cache[l], cache_dtype=cache_dtype,
-                        cache_len=self.cache[l].shape[1])
-      ops.gemm(self.xn, L.qkv, ep, out=self.q)
+      rope = dict(heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin, places=self.places,
+                  cache_rows=self.rows, cache=self.cache[l], cache_dtype=cache_dtype, cache_len=self.cache[l].shape[1])
+      if l == 0:
+        ops.rms_rows(self.x, L.norm1, c.eps, c.centered, out=self.xn)
+        ops.gemm(self.xn, L.qkv, ops.epilogue(lib.EP_ROPE_KV, **rope), out=self.q)
+      else:
+        ops.gemm(self.xn, L.qkv, ops.epilogue(lib.EP_ROPE_KV, **rs, **rope), out=self.q)
       ops.attention_decode(self.q, self.cache[l], c.heads, c.kv, hd, self.places, self.first, self.context, self.ws, o=self.att)
-      ops.gemm(self.att, L.o, ops.epilogue(lib.EP_RESIDUAL, residual=self.x), out=self.x)
-      ops.rms_rows(self.x, L.norm2, c.eps, c.centered, out=self.xn)
-      ops.gemm(self.xn, L.gate_up, ops.epilogue(lib.EP_SILU_GATE, split=c.ffn), out=self.hb)
-      ops.gemm(self.hb, L.down, ops.epilogue(lib.EP_RESIDUAL, residual=self.x), out=self.x)
-    ops.rms_rows(self.x, self.norm, c.eps, c.centered, out=self.xn)
-    ops.gemm(self.xn, self.head, ops.epilogue(lib.EP_STORE, argmax_parts=self.parts), out=self.logits)
+      ops.gemm(self.att, L.o, ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq, copy_bf16=self.xn,
+                                           copy_w=nw[2 * l + 1]), out=self.x)
+      ops.gemm(self.xn, L.gate_up, ops.epilogue(lib.EP_SILU_GATE, split=c.ffn, **rs), out=self.hb)
+      ops.gemm(self.hb, L.down, ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq, copy_bf16=self.xn,
+                                             copy_w=nw[2 * l + 2]), out=self.x)
+    ops.gemm(self.xn, self.head, ops.epilogue(lib.EP_STORE, argmax_parts=self.parts, **rs), out=self.logits)
     ops.argmax_parts(self.parts, self.picks)
 
   def _prefill_buffers(self, T):
@@ -235,6 +250,8 @@ class Decoder:
     rows.copy_(places + slot * self.part)
     cache_dtype = lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"]
     ops.embed_rows(self.embed, ids_t, x, ssq)
+    # (each RMSNorm a pass of its own here: at 2048 rows the tiled kernel's per-tile sums of the rows' squares cost
+    # more than fh_rms_rows; the batched decode takes the residual epilogues' scaled copies instead)
     for l, L in enumerate(self.layers):
       ops.rms_rows(x, L.norm1, c.eps, c.centered, out=xn)
       ep = ops.epilogue(lib.EP_ROPE_KV, heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,

@@ -109,7 +109,9 @@ typedef struct fh_epilogue {
   int kind;                 /* FH_EP_* */
   /* RMSNorm prologue (models/llama.py:82-85): x is replaced by x * rsqrt(mean(x^2) + eps) * w (n*w + n if centered).
    * The mean comes from ssq_in: per row, the sums of x^2 over each run of 16 columns ([batch][K/16]), which the
-   * kernel that made x wrote (FH_EP_RESIDUAL's ssq_out, fh_embed_rows). norm_w NULL: no prologue. */
+   * kernel that made x wrote (FH_EP_RESIDUAL's ssq_out, fh_embed_rows). norm_w NULL and ssq_in NULL: no prologue.
+   * norm_w NULL with ssq_in: x's rows already hold x * w (FH_EP_RESIDUAL's copy_bf16 with copy_w), and each row is
+   * scaled by rsqrt(mean(x^2) + eps) only, the mean of the unscaled rows that ssq_in holds. */
   const float* norm_w;      /* [K] */
   const float* ssq_in;      /* [batch][K/16] */
   float eps;
@@ -133,6 +135,13 @@ typedef struct fh_epilogue {
   void* argmax_parts;
   /* FH_EP_PROGRAM: the program, evaluated at each output (batch row, column) with the matmul's result as its acc */
   const struct fh_program* program;
+  /* FH_EP_RESIDUAL: y also written as bf16 ([batch][N], row stride N; nearest even), times copy_w [N] where given
+   * (the next RMSNorm's weight, its centered + 1 included): the next matmul's rows, which it takes with ssq_in =
+   * this epilogue's ssq_out and norm_w NULL; or NULL. No counterpart in the reference: it saves the separate
+   * normalising pass before a matrix-core matmul, and the products are the same as its RMSNorm prologue's
+   * (bf16(x * w), then 1/rms on the sums). */
+  void* copy_bf16;
+  const float* copy_w;
 } fh_epilogue;
 
 /* y (dtype y_dtype, row stride ldy) from x @ W and the epilogue. x: fp32. w_mant/w_exps: a packed [K][N] weight

@@ -105,11 +105,30 @@ def test_gemm_epilogues(cuda, M):
   res = rng.normal(0, 1, (M, c.dim)).astype(np.float32)
   y, s = to_gpu(res.copy()), torch.zeros(M, c.dim // 16, device="cuda")
   xb = O.bf16(x).astype(np.float64)
-  ops().gemm(to_gpu(x), ops().pack(to_gpu(w)), ops().epilogue(L.EP_RESIDUAL, residual=y, ssq_out=s), out=y)
+  cp = torch.zeros(M, c.dim, dtype=torch.bfloat16, device="cuda")
+  bw = ops().pack(to_gpu(w))
+  ops().gemm(to_gpu(x), bw, ops().epilogue(L.EP_RESIDUAL, residual=y, ssq_out=s, copy_bf16=cp), out=y)
   want = res + xb @ wv
   within(y.cpu().numpy(), want, 1e-5 * (np.abs(xb) @ np.abs(wv)) + 1e-6, "residual")
   north_star(y.cpu().numpy(), res + x @ wv, "residual")
   assert np.allclose(s.cpu().numpy(), (y.cpu().numpy().astype(np.float64).reshape(M, -1, 16) ** 2).sum(-1), rtol=1e-5)
+  # the rows again in bf16 (nearest even) for the next matmul; the GEMV's epilogue writes the same
+  assert np.array_equal(cp.float().cpu().numpy(), O.bf16(y.cpu().numpy()))
+  yv, cv = to_gpu(res.copy()), torch.zeros(M, c.dim, dtype=torch.bfloat16, device="cuda")
+  ops().gemv(to_gpu(x), bw, ops().epilogue(L.EP_RESIDUAL, residual=yv, copy_bf16=cv), out=yv)
+  assert np.array_equal(cv.float().cpu().numpy(), O.bf16(yv.cpu().numpy()))
+  with pytest.raises(ValueError):  # a copy is the residual epilogue's
+    ops().gemm(to_gpu(x), bw, ops().epilogue(L.EP_STORE, copy_bf16=cv))
+  # the copy times the next RMSNorm's weight, and a matmul of those rows with 1/rms alone (ssq_in without norm_w):
+  # the same products as the RMSNorm prologue on the fp32 rows, bf16(x w), so the same result
+  gw = to_gpu(g.reshape(-1))
+  yw, cw, sw = to_gpu(res.copy()), torch.zeros(M, c.dim, dtype=torch.bfloat16, device="cuda"), torch.zeros(M, c.dim // 16, device="cuda")
+  ops().gemm(to_gpu(x), bw, ops().epilogue(L.EP_RESIDUAL, residual=yw, ssq_out=sw, copy_bf16=cw, copy_w=gw), out=yw)
+  assert np.array_equal(cw.float().cpu().numpy(), O.bf16(yw.cpu().numpy() * g))
+  w2 = ops().pack(to_gpu(rng.normal(0, 0.02, (c.dim, 256)).astype(np.float32)))
+  a1 = ops().gemm(yw, w2, ops().epilogue(L.EP_STORE, norm_w=gw, ssq_in=sw, eps=c.eps))
+  a2 = ops().gemm(cw, w2, ops().epilogue(L.EP_STORE, ssq_in=sw, eps=c.eps))
+  assert torch.equal(a1, a2)
   # RMSNorm prologue, store with the argmax pairs
   parts = torch.zeros(M, c.dim // 16, dtype=torch.int64, device="cuda")
   ep = ops().epilogue(L.EP_STORE, norm_w=to_gpu(g.reshape(-1)), ssq_in=to_gpu(ssq), eps=c.eps, argmax_parts=parts)
