@@ -74,18 +74,19 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
     }
     scale_s[t] = sc;
   }
-  // each row's 1 / rms from the sums of squares its maker left by runs of 16: wave w the rows w, w + W, ..
-  for (int row = wave; row < 16 * MB; row += W) {
-    float r = 1.f;
-    if (a.ssq_in && row < M) {  // (NORM, or rows that already hold x * w)
-      const float* q = a.ssq_in + xrow(row) * a.ssq_parts;
-      float s = 0.f;
-      for (int i = lane; i < a.ssq_parts; i += 64) s += q[i];
-      s = wave_sum(s);
-      r = 1.0f / sqrtf(s / (float)K + a.eps);
-    }
-    if (lane == 0) rs_s[row] = r;
-  }
+  // each row's sums of squares (its maker left them by runs of 16), spread over the workgroup's threads (tpr
+  // consecutive lanes a row): loaded now, summed into 1 / rms after the stream, so that the loads overlap it
+  int tpr = 1;  // (the largest power of 2 that the workgroup's threads give each row, at most 64: within a wave;
+                // W need not be a power of 2, and threads past tpr 16 MB take no row)
+  while (tpr < 64 && tpr * 2 * 16 * MB <= (int)blockDim.x) tpr *= 2;
+  const int srow = t / tpr, sk = t % tpr;
+  constexpr int SQ = 8;
+  const bool has_ssq = a.ssq_in != nullptr && M > 0;
+  const float* sqp = has_ssq ? a.ssq_in + xrow(min(srow, M - 1)) * a.ssq_parts : (const float*)a.x;
+  const int sqn = has_ssq ? a.ssq_parts : 1;
+  float sq[SQ];
+#pragma unroll
+  for (int i = 0; i < SQ; ++i) sq[i] = sqp[min(sk + tpr * i, sqn - 1)];
   __syncthreads();
 
   // the item's two runs
@@ -222,6 +223,16 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
         load_w(k + SK_RING * SK_BK, wr[i], we[i]);
       }
     }
+  }
+
+  // each row's 1 / rms (1 past M or without ssq_in)
+  {
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < SQ; ++i) sum += sk + tpr * i < sqn ? sq[i] : 0.f;
+    for (int i = SQ * tpr + sk; i < sqn; i += tpr) sum += sqp[i];  // (more runs than SQ tpr)
+    for (int m = tpr >> 1; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
+    if (sk == 0 && srow < 16 * MB) rs_s[srow] = (has_ssq && srow < M) ? 1.0f / sqrtf(sum / (float)K + a.eps) : 1.f;
   }
 
   // the waves' sums meet in LDS, in wave order: block b, run j's value i of lane l is row 16 b + 4 (l / 16) + i,
