@@ -2,8 +2,8 @@
 // and a mixture of experts' expert matmuls. y = epilogue(prologue(x) @ W), with fh_gemm_bfp's arithmetic (x times the
 // RMSNorm weight rounded to bf16, the weight's values exact, fp32 sums).
 //
-// Built like the decode GEMV: a workgroup takes one item of 32 columns (two runs of 16, or a RoPE / SiLU·gate pair)
-// and its W waves split K; nothing crosses workgroups. A wave walks its K slice 64 rows at a time and reads the
+// Built like the decode GEMV: a workgroup takes one item of 32 columns (two runs of 16, or a RoPE / SiLU·gate pair;
+// one run of 16 where items of two would leave CUs idle) and its W waves split K; nothing crosses workgroups. A wave walks its K slice 64 rows at a time and reads the
 // weight as the GEMV does: a lane a row of a run (16 bytes of bfp8, 8 of bfp4, and its exponent byte), a wave's loads
 // 1 KiB (512 B) contiguous, four steps of them in flight. A lane turns its row into 16 bf16 values and writes them
 // row-major into the wave's own LDS tile (no workgroup barrier in the loop: a wave reads back only what it wrote);
@@ -40,7 +40,7 @@ __device__ inline uint32_t sk_pack_exact(float lo, float hi) {
 // threads a workgroup at most: fewer where a lane holds more, so that registers do not spill
 __host__ __device__ constexpr int skinny_threads(bool xbf16, int mb) { return (xbf16 && mb == 1) ? 1024 : 512; }
 
-template <bool FOUR, bool XBF16, bool NORM, int MB>  // MB: blocks of 16 rows
+template <bool FOUR, bool XBF16, bool NORM, int MB, int R>  // MB: blocks of 16 rows; R: runs of 16 columns an item
 __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatArgs a, SkinnyMoe moe) {
   constexpr int RB = FOUR ? 8 : 16;
   constexpr int XW = XBF16 ? 1 : 2;    // 16-byte loads for 8 of x's values
@@ -91,25 +91,27 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
 
   // the item's two runs
   int64_t nb[2];
-  if (a.P == 1) { nb[0] = 2 * (int64_t)item; nb[1] = nb[0] + 1; }
+  if (R == 1) { nb[0] = item; nb[1] = item; }
+  else if (a.P == 1) { nb[0] = 2 * (int64_t)item; nb[1] = nb[0] + 1; }
   else { nb[0] = pair_first(item, a.pair_half); nb[1] = nb[0] + a.pair_half; }
-  const bool run1_ok = nb[1] < a.N / 16;  // (P == 1 with an odd count of runs: the last item's second run is absent)
+  // (P == 1 with an odd count of runs: the last item's second run is absent)
+  const bool run1_ok = R == 2 && nb[1] < a.N / 16;
   const uint8_t* mant = a.mant + (int64_t)e * moe.expert_mant;
   const uint8_t* exps = a.exps + (int64_t)e * moe.expert_exps;
 
-  floatx4 acc[MB][2];  // [16-row block][run]: lane l holds rows 4 (l / 16) + i, column l % 16 of the run
+  floatx4 acc[MB][R];  // [16-row block][run]: lane l holds rows 4 (l / 16) + i, column l % 16 of the run
 #pragma unroll
   for (int b = 0; b < MB; ++b)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[b][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < R; ++j) acc[b][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   uint16_t* Bs = (uint16_t*)sk_smem + wave * SK_TILE;
   const int r0 = wave * a.rows, r1 = min(K, r0 + a.rows);
   if (any_s && r0 < r1) {
-    const uint8_t* mrun[2];
-    const uint8_t* erun[2];
+    const uint8_t* mrun[R];
+    const uint8_t* erun[R];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < R; ++j) {
       const int64_t run = (j == 1 && !run1_ok) ? nb[0] : nb[j];
       mrun[j] = mant + run * a.K * RB;
       erun[j] = exps + run * a.K;
@@ -125,13 +127,13 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
     const int g = lane >> 4, m4 = (lane & 15) >> 2, q4 = lane & 3;
     FH_LDS short4v* trp = (FH_LDS short4v*)(Bs + (8 * g + m4) * SK_RS + 4 * q4);
 
-    Row wr[SK_RING][2];
-    uint32_t we[SK_RING][2];
-    auto load_w = [&](int k0, Row (&w)[2], uint32_t (&ex)[2]) {
+    Row wr[SK_RING][R];
+    uint32_t we[SK_RING][R];
+    auto load_w = [&](int k0, Row (&w)[R], uint32_t (&ex)[R]) {
       __builtin_amdgcn_sched_barrier(0);
       const int k = min(k0, last) + lane;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) { w[j] = *(const Row*)(mrun[j] + (uint32_t)k * RB); ex[j] = erun[j][(uint32_t)k]; }
+      for (int j = 0; j < R; ++j) { w[j] = *(const Row*)(mrun[j] + (uint32_t)k * RB); ex[j] = erun[j][(uint32_t)k]; }
       __builtin_amdgcn_sched_barrier(0);
     };
     uint4 xv[2][MB][2][XW];  // [set][block][k32 half][16 bytes]
@@ -148,10 +150,10 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
         }
       __builtin_amdgcn_sched_barrier(0);
     };
-    auto step = [&](int k0, bool valid, const Row (&w)[2], const uint32_t (&ex)[2], const uint4 (&xs)[MB][2][XW]) {
-      // the lane's two rows -> 16 bf16 values each, row-major into the tile (rows past the slice: zero)
+    auto step = [&](int k0, bool valid, const Row (&w)[R], const uint32_t (&ex)[R], const uint4 (&xs)[MB][2][XW]) {
+      // the lane's rows of the R runs -> 16 bf16 values each, row-major into the tile (rows past the slice: zero)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < R; ++j) {
         float f[16];
         magnitudes(w[j], f);
         const float sc = valid ? ldexpf(1.f, (int)ex[j] - 133) : 0.f;
@@ -167,9 +169,9 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
       for (int h = 0; h < 2; ++h) {  // the step's two blocks of 32 k
-        bf16x8 bfr[2];
+        bf16x8 bfr[R];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < R; ++j) {
           const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(trp + (32 * h * SK_RS + 16 * j) / 4);
           const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(trp + (32 * h * SK_RS + 4 * SK_RS + 16 * j) / 4);
           const short v8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
             for (int j = 0; j < 8; ++j) af[j] = (__bf16)(NORM ? v[j] * gw[j] : v[j]);
           }
 #pragma unroll
-          for (int j = 0; j < 2; ++j) acc[b][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[j], acc[b][j], 0, 0, 0);
+          for (int j = 0; j < R; ++j) acc[b][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[j], acc[b][j], 0, 0, 0);
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -243,10 +245,10 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
 #pragma unroll
   for (int b = 0; b < MB; ++b)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)  // (R == 1: the second run's columns are zeros, never stored)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        part[(wave * 16 * MB + 16 * b + 4 * (lane >> 4) + i) * PLD + 16 * j + (lane & 15)] = acc[b][j][i];
+        part[(wave * 16 * MB + 16 * b + 4 * (lane >> 4) + i) * PLD + 16 * j + (lane & 15)] = j < R ? acc[b][j < R ? j : 0][i] : 0.f;
   __syncthreads();
   float* fin = part + W * 16 * MB * PLD;  // [16 MB][33]
   for (int i = t; i < 16 * MB * 32; i += blockDim.x) {
@@ -333,21 +335,29 @@ static void skinny_plan(int64_t K, int items, int experts, int most, int& W, int
   rows = (int)r;
 }
 
-template <bool FOUR, bool XBF16, bool NORM>
+template <bool FOUR, bool XBF16, bool NORM, int R>
 static void skinny_launch(const MatArgs& a, const SkinnyMoe& moe, int items, int experts, int W, int mb, hipStream_t s) {
   const dim3 g(items, experts), b(64 * W);
   const size_t lds = (size_t)(W + 1) * 16 * mb * 33 * 4;  // the sums' tiles (they reuse the weight tiles)
   const size_t tiles = (size_t)W * SK_TILE * 2;
   const size_t bytes = lds > tiles ? lds : tiles;
-  if (mb == 1) hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 1>), g, b, bytes, s, a, moe);
-  else if (mb == 2) hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 2>), g, b, bytes, s, a, moe);
-  else hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 4>), g, b, bytes, s, a, moe);
+  if (mb == 1) hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 1, R>), g, b, bytes, s, a, moe);
+  else if (mb == 2) hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 2, R>), g, b, bytes, s, a, moe);
+  else hipLaunchKernelGGL((skinny_kernel<FOUR, XBF16, NORM, 4, R>), g, b, bytes, s, a, moe);
+}
+
+template <bool FOUR, bool XBF16, bool NORM>
+static void skinny_runs(const MatArgs& a, const SkinnyMoe& moe, bool one, int items, int experts, int W, int mb, hipStream_t s) {
+  if (one) skinny_launch<FOUR, XBF16, NORM, 1>(a, moe, items, experts, W, mb, s);
+  else skinny_launch<FOUR, XBF16, NORM, 2>(a, moe, items, experts, W, mb, s);
 }
 
 // M rows (at most 64 a pass) of a [grouped] skinny matmul; the caller checked the epilogue
 int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts, hipStream_t s) {
   if (a0.K % 64) return fail(FH_EUNSUP, "skinny matmul: K a multiple of 64");
-  const int items = (int)(a0.P == 1 ? (a0.N / 16 + 1) / 2 : a0.items);
+  // an item is two runs (32 columns), or one where two a workgroup would leave CUs idle (P == 1, under 256 items)
+  const bool one = a0.P == 1 && (a0.N / 32) * (int64_t)experts < 256;
+  const int items = (int)(one ? a0.N / 16 : a0.P == 1 ? (a0.N / 16 + 1) / 2 : a0.items);
   if (experts > 256) return fail(FH_EUNSUP, "skinny matmul: at most 256 experts");
   int W, rows;
   const int mb0 = a0.M > 32 ? 4 : a0.M > 16 ? 2 : 1;
@@ -369,14 +379,14 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
     const int mb = a.M > 32 ? 4 : a.M > 16 ? 2 : 1;
     const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
     switch (which) {
-      case 0: skinny_launch<false, false, false>(a, mo, items, experts, W, mb, s); break;
-      case 1: skinny_launch<false, false, true>(a, mo, items, experts, W, mb, s); break;
-      case 2: skinny_launch<false, true, false>(a, mo, items, experts, W, mb, s); break;
-      case 3: skinny_launch<false, true, true>(a, mo, items, experts, W, mb, s); break;
-      case 4: skinny_launch<true, false, false>(a, mo, items, experts, W, mb, s); break;
-      case 5: skinny_launch<true, false, true>(a, mo, items, experts, W, mb, s); break;
-      case 6: skinny_launch<true, true, false>(a, mo, items, experts, W, mb, s); break;
-      default: skinny_launch<true, true, true>(a, mo, items, experts, W, mb, s); break;
+      case 0: skinny_runs<false, false, false>(a, mo, one, items, experts, W, mb, s); break;
+      case 1: skinny_runs<false, false, true>(a, mo, one, items, experts, W, mb, s); break;
+      case 2: skinny_runs<false, true, false>(a, mo, one, items, experts, W, mb, s); break;
+      case 3: skinny_runs<false, true, true>(a, mo, one, items, experts, W, mb, s); break;
+      case 4: skinny_runs<true, false, false>(a, mo, one, items, experts, W, mb, s); break;
+      case 5: skinny_runs<true, false, true>(a, mo, one, items, experts, W, mb, s); break;
+      case 6: skinny_runs<true, true, false>(a, mo, one, items, experts, W, mb, s); break;
+      default: skinny_runs<true, true, true>(a, mo, one, items, experts, W, mb, s); break;
     }
     if (int rc = check_launch("skinny matmul")) return rc;
   }
