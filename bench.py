@@ -57,11 +57,10 @@ def gemv_rates(dec, stream, reps=5):
   the packed weight, x and the norm's weights read once, y written once."""
   from ferrite_amd import lib, ops
   c, B = dec.c, dec.batch
-  cache_dtype = lib.DTYPES["bf16" if dec.kv_dtype == torch.bfloat16 else "fp32"]
   calls = {
     "qkv": [(dec.x, L.qkv, lambda L=L, l=l: ops.epilogue(lib.EP_ROPE_KV, norm_w=L.norm1, ssq_in=dec.ssq, eps=c.eps, heads=c.heads,
              kv_heads=c.kv, head_dim=dec.hd, cos_tab=dec.cos, sin_tab=dec.sin, places=dec.places, cache_rows=dec.rows,
-             cache=dec.cache[l], cache_dtype=cache_dtype, cache_len=dec.cache[l].shape[1]), dec.q, c.dim * 4)
+             **dec._cache(l)), dec.q, c.dim * 4)
             for l, L in enumerate(dec.layers)],
     "o": [(dec.att, L.o, lambda: ops.epilogue(lib.EP_RESIDUAL, residual=dec.x, ssq_out=dec.ssq), dec.x, 0) for L in dec.layers],
     "gate_up": [(dec.x, L.gate_up, lambda L=L: ops.epilogue(lib.EP_SILU_GATE, norm_w=L.norm2, ssq_in=dec.ssq, eps=c.eps, split=c.ffn),

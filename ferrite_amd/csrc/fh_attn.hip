@@ -8,8 +8,10 @@
 // chunks of each (row, head): a thread a chunk's statistics and a dimension's values, all loaded in one round with the
 // row's place, one exp(max - the largest) a thread. A kernel boundary, not a fence, orders the two: on MI355X an
 // agent-scope release (an L2 write-back on each XCD) and a counter cost more than the ~1.4 us boundary. A row reads
-// only the cache rows its place reaches.
+// only the cache rows its place reaches. A block-float cache (bfp8 or bfp4) is decoded into the same bf16 tiles as it
+// is loaded, exactly (a run's values are bf16 values), so its results are bit for bit a bf16 cache's of those values.
 #include <math.h>
+#include <type_traits>
 #include "fh_common.h"
 
 namespace fh {
@@ -18,7 +20,7 @@ constexpr int ATT_CHUNK = 64;                // cache rows a workgroup (a lane a
 constexpr int ATT_REP = 16;                  // query heads a key head, at most (a wave each)
 
 struct AttArgs {
-  const float* q; const void* cache; int64_t cache_len;
+  const float* q; const void* cache; int64_t cache_len; const uint8_t* cache_exps;
   int heads, kv_heads; float scale;
   const int32_t* places; const int32_t* first_row;
   int max_chunks;
@@ -41,10 +43,12 @@ static size_t att_lds(int hd, int es, int rep) {
   return (size_t)2 * ATT_CHUNK * att_row_bytes(hd, es) + (size_t)rep * hd * 4 + (size_t)rep * ATT_CHUNK * 4;
 }
 
-template <int HD, bool BF>
+template <int HD, int CF>
 __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(AttArgs a) {
+  constexpr bool BF = CF != FH_F32;            // the tiles in bf16 (a bf16 or block-float cache)
   constexpr int DL = HD / 64;                  // dimensions a lane (p v, the combine)
-  constexpr int ES = BF ? 2 : 4;               // bytes an element
+  constexpr int ES = BF ? 2 : 4;               // bytes an element in LDS
+  constexpr int V16 = HD * ES / 16;            // 16-byte pieces a row in LDS
   constexpr int RW = att_row_bytes(HD, ES);    // (16 more than the row: a lane's 16-byte reads of its own row spread
                                                // over the banks)
   extern __shared__ __attribute__((aligned(16))) char att_smem[];
@@ -63,33 +67,74 @@ __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(AttArgs a) {
   float* qs = (float*)(att_smem + 2 * ATT_CHUNK * RW);
   float* ps = qs + rep * HD + wave * ATT_CHUNK;  // this wave's p
 
-  // the chunk's keys and values into LDS, 16 bytes a thread a piece, and the heads' q: every load issued before any
-  // LDS store (rows past n read the last row, unused; pieces past the chunk read its last piece again)
-  constexpr int V16 = HD * ES / 16;            // 16-byte pieces a row
-  constexpr int PIECES = ATT_CHUNK * V16;
-  const char* kb = (const char*)a.cache + ((int64_t)kvh * a.cache_len + row0 + c0) * HD * ES;
-  const char* vb = (const char*)a.cache + ((int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + c0) * HD * ES;
   const float* qrow = a.q + ((int64_t)b * a.heads + (int64_t)kvh * rep) * HD;
-  for (int i0 = 0; i0 < PIECES; i0 += 4 * nthreads) {
-    uint4 kp[4], vp[4];
-    float4 qp = make_float4(0.f, 0.f, 0.f, 0.f);
+  if constexpr (CF == FH_F32 || CF == FH_BF16) {
+    // the chunk's keys and values into LDS, 16 bytes a thread a piece, and the heads' q: every load issued before any
+    // LDS store (rows past n read the last row, unused; pieces past the chunk read its last piece again)
+    constexpr int PIECES = ATT_CHUNK * V16;
+    const char* kb = (const char*)a.cache + ((int64_t)kvh * a.cache_len + row0 + c0) * HD * ES;
+    const char* vb = (const char*)a.cache + ((int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + c0) * HD * ES;
+    for (int i0 = 0; i0 < PIECES; i0 += 4 * nthreads) {
+      uint4 kp[4], vp[4];
+      float4 qp = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = min(i0 + u * nthreads + tid, PIECES - 1);
-      const int r = i / V16, pc = i % V16, rr = r < n ? r : n - 1;
-      kp[u] = *(const uint4*)(kb + (int64_t)rr * HD * ES + 16 * pc);
-      vp[u] = *(const uint4*)(vb + (int64_t)rr * HD * ES + 16 * pc);
-    }
-    if (i0 == 0) qp = *(const float4*)(qrow + 4 * min(tid, rep * HD / 4 - 1));  // (rep HD / 4 <= 16 HD / 4 <= 64 rep)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = i0 + u * nthreads + tid;
-      if (i < PIECES) {
-        *(uint4*)(ks + (i / V16) * RW + 16 * (i % V16)) = kp[u];
-        *(uint4*)(vs + (i / V16) * RW + 16 * (i % V16)) = vp[u];
+      for (int u = 0; u < 4; ++u) {
+        const int i = min(i0 + u * nthreads + tid, PIECES - 1);
+        const int r = i / V16, pc = i % V16, rr = r < n ? r : n - 1;
+        kp[u] = *(const uint4*)(kb + (int64_t)rr * HD * ES + 16 * pc);
+        vp[u] = *(const uint4*)(vb + (int64_t)rr * HD * ES + 16 * pc);
       }
+      if (i0 == 0) qp = *(const float4*)(qrow + 4 * min(tid, rep * HD / 4 - 1));  // (rep HD / 4 <= 16 HD / 4 <= 64 rep)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * nthreads + tid;
+        if (i < PIECES) {
+          *(uint4*)(ks + (i / V16) * RW + 16 * (i % V16)) = kp[u];
+          *(uint4*)(vs + (i / V16) * RW + 16 * (i % V16)) = vp[u];
+        }
+      }
+      if (i0 == 0 && tid < rep * HD / 4) *(float4*)(qs + 4 * tid) = qp;
     }
-    if (i0 == 0 && tid < rep * HD / 4) *(float4*)(qs + 4 * tid) = qp;
+  } else {
+    // a block float: a thread a run of 16 (its magnitudes and exponent byte) a piece, decoded to bf16 into LDS
+    // (32 bytes), the same order of loads then stores
+    using Run = typename std::conditional<CF == FH_BFP8, uint4, uint2>::type;
+    constexpr int RUNS = HD / 16, PIECES = ATT_CHUNK * RUNS;
+    const int64_t kr = (int64_t)kvh * a.cache_len + row0 + c0, vr = (int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + c0;
+    const Run* km = (const Run*)a.cache + kr * RUNS;
+    const Run* vm = (const Run*)a.cache + vr * RUNS;
+    const uint8_t* ke = a.cache_exps + kr * RUNS;
+    const uint8_t* ve = a.cache_exps + vr * RUNS;
+    for (int i0 = 0; i0 < PIECES; i0 += 4 * nthreads) {
+      Run kp[4], vp[4];
+      uint32_t kx[4], vx[4];
+      float4 qp = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = min(i0 + u * nthreads + tid, PIECES - 1);
+        const int r = i / RUNS, pc = i % RUNS, rr = r < n ? r : n - 1;
+        kp[u] = km[rr * RUNS + pc]; kx[u] = ke[rr * RUNS + pc];
+        vp[u] = vm[rr * RUNS + pc]; vx[u] = ve[rr * RUNS + pc];
+      }
+      if (i0 == 0) qp = *(const float4*)(qrow + 4 * min(tid, rep * HD / 4 - 1));
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * nthreads + tid;
+        if (i < PIECES) {
+          float f[16];
+          uint32_t w[8];
+          uint4* kd = (uint4*)(ks + (i / RUNS) * RW + 32 * (i % RUNS));
+          uint4* vd = (uint4*)(vs + (i / RUNS) * RW + 32 * (i % RUNS));
+          magnitudes(kp[u], f);
+          bfp_run_bf16<16>(f, kx[u], w);
+          kd[0] = make_uint4(w[0], w[1], w[2], w[3]); kd[1] = make_uint4(w[4], w[5], w[6], w[7]);
+          magnitudes(vp[u], f);
+          bfp_run_bf16<16>(f, vx[u], w);
+          vd[0] = make_uint4(w[0], w[1], w[2], w[3]); vd[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        }
+      }
+      if (i0 == 0 && tid < rep * HD / 4) *(float4*)(qs + 4 * tid) = qp;
+    }
   }
   __syncthreads();
 
@@ -133,7 +178,7 @@ __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(AttArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const char* vr = vs + (4 * t4 + u) * RW + DL * ES * lane;
-      if (BF && DL == 2) {
+      if constexpr (BF && DL == 2) {
         const uint32_t w = *(const uint32_t*)vr;
         o[0] = fmaf(pt[u], __uint_as_float(w << 16), o[0]);
         o[1] = fmaf(pt[u], __uint_as_float(w & 0xFFFF0000u), o[1]);
@@ -221,12 +266,23 @@ __global__ __launch_bounds__(HD) void attention_combine(AttArgs a) {
 }
 
 // the kernel, allowed its largest LDS (above 64 KiB for fp32 rows of 256 and 16 heads a key head) once
-template <int HD, bool BF>
+template <int HD, int CF>
 static void launch_attention(dim3 grid, dim3 block, size_t lds, hipStream_t s, const AttArgs& a) {
-  static const hipError_t allowed = hipFuncSetAttribute((const void*)attention_kernel<HD, BF>,
-      hipFuncAttributeMaxDynamicSharedMemorySize, (int)att_lds(HD, BF ? 2 : 4, ATT_REP));
+  static const hipError_t allowed = hipFuncSetAttribute((const void*)attention_kernel<HD, CF>,
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)att_lds(HD, CF == FH_F32 ? 4 : 2, ATT_REP));
   (void)allowed;  // (a refusal shows as the launch's error)
-  hipLaunchKernelGGL((attention_kernel<HD, BF>), grid, block, lds, s, a);
+  hipLaunchKernelGGL((attention_kernel<HD, CF>), grid, block, lds, s, a);
+}
+
+template <int HD>
+static void launch_attention(int cf, dim3 grid, dim3 block, size_t lds, hipStream_t s, const AttArgs& a) {
+  switch (cf) {
+    case FH_F32: launch_attention<HD, FH_F32>(grid, block, lds, s, a); break;
+    case FH_BF16: launch_attention<HD, FH_BF16>(grid, block, lds, s, a); break;
+    case FH_BFP8: launch_attention<HD, FH_BFP8>(grid, block, lds, s, a); break;
+    default: launch_attention<HD, FH_BFP4>(grid, block, lds, s, a); break;
+  }
+  if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<HD>, dim3(a.heads, grid.z), dim3(HD), 0, s, a);
 }
 
 }  // namespace fh
@@ -239,6 +295,17 @@ extern "C" size_t fh_attention_workspace_bytes(int batch, int heads, int head_di
   return (size_t)batch * heads * chunks * (head_dim + 2) * sizeof(float);
 }
 
+extern "C" size_t fh_kv_cache_bytes(int cache_dtype, int kv_heads, int64_t cache_len, int head_dim) {
+  if (kv_heads < 1 || cache_len < 1 || head_dim < 32 || head_dim % 32) return 0;
+  const int64_t rows = 2 * (int64_t)kv_heads * cache_len;
+  switch (cache_dtype) {
+    case FH_F32: return (size_t)rows * head_dim * 4;
+    case FH_BF16: return (size_t)rows * head_dim * 2;
+    case FH_BFP8: case FH_BFP4: return (size_t)(kv_exps_at(cache_dtype, kv_heads, cache_len, head_dim) + rows * (head_dim / 16));
+    default: return 0;
+  }
+}
+
 extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch,
                                    int heads, int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row,
                                    int64_t max_context, float* o, void* workspace, size_t ws_bytes, void* stream) {
@@ -247,13 +314,15 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
     return fail(FH_EINVAL, "fh_attention_decode: heads must be a multiple of kv_heads");
   if (heads / kv_heads > ATT_REP) return fail(FH_EUNSUP, "fh_attention_decode: at most 16 query heads a key head");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(FH_EUNSUP, "fh_attention_decode: head_dim 64, 128 or 256");
-  if (cache_dtype != FH_F32 && cache_dtype != FH_BF16) return fail(FH_EUNSUP, "fh_attention_decode: cache is FH_F32 or FH_BF16");
+  if (cache_dtype < FH_F32 || cache_dtype > FH_BFP4)
+    return fail(FH_EUNSUP, "fh_attention_decode: cache is FH_F32, FH_BF16, FH_BFP8 or FH_BFP4");
   if (max_context < 1 || max_context > cache_len) return fail(FH_EINVAL, "fh_attention_decode: max_context outside 1..cache_len");
   const size_t need = fh_attention_workspace_bytes(batch, heads, head_dim, max_context);
   if (max_context > ATT_CHUNK && (!workspace || ws_bytes < need))
     return fail(FH_EINVAL, "fh_attention_decode: workspace smaller than fh_attention_workspace_bytes");
   AttArgs a;
   a.q = q; a.cache = cache; a.cache_len = cache_len;
+  a.cache_exps = (const uint8_t*)cache + kv_exps_at(cache_dtype, kv_heads, cache_len, head_dim);
   a.heads = heads; a.kv_heads = kv_heads; a.scale = 1.0f / sqrtf((float)head_dim);
   a.places = places; a.first_row = first_row;
   a.max_chunks = (int)((max_context + ATT_CHUNK - 1) / ATT_CHUNK);
@@ -261,17 +330,12 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   a.part = (float*)workspace;
   const int rep = heads / kv_heads;
   const dim3 grid(a.max_chunks, kv_heads, batch), block(64 * rep);
-  const bool bf = cache_dtype == FH_BF16;
-  const size_t lds = att_lds(head_dim, bf ? 2 : 4, rep);
+  const size_t lds = att_lds(head_dim, cache_dtype == FH_F32 ? 4 : 2, rep);
   hipStream_t s = as_stream(stream);
-  const dim3 cgrid(heads, batch);
   switch (head_dim) {
-    case 64: if (bf) launch_attention<64, true>(grid, block, lds, s, a); else launch_attention<64, false>(grid, block, lds, s, a);
-             if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<64>, cgrid, dim3(64), 0, s, a); break;
-    case 128: if (bf) launch_attention<128, true>(grid, block, lds, s, a); else launch_attention<128, false>(grid, block, lds, s, a);
-              if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<128>, cgrid, dim3(128), 0, s, a); break;
-    default: if (bf) launch_attention<256, true>(grid, block, lds, s, a); else launch_attention<256, false>(grid, block, lds, s, a);
-             if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<256>, cgrid, dim3(256), 0, s, a); break;
+    case 64: launch_attention<64>(cache_dtype, grid, block, lds, s, a); break;
+    case 128: launch_attention<128>(cache_dtype, grid, block, lds, s, a); break;
+    default: launch_attention<256>(cache_dtype, grid, block, lds, s, a); break;
   }
   return check_launch("fh_attention_decode");
 }

@@ -49,6 +49,65 @@ __host__ __device__ inline uint32_t bfp_value_bf16(int32_t sq, uint32_t top) {
   return (s << 15) | out;
 }
 
+// the 16 magnitudes of a run's row as floats: bfp8's 16 bytes are the signed q; bfp4's 8 bytes give 16 q (the 16 is
+// folded into the scale: q * 2^(e - 129) = 16 q * 2^(e - 133))
+__device__ inline void magnitudes(const uint4& m, float (&f)[16]) {
+  const uint32_t w[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) f[j] = (float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 255u);
+}
+__device__ inline void magnitudes(const uint2& m, float (&f)[16]) {
+  const uint32_t w[2] = {m.x, m.y};
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const uint32_t hi = w[d] & 0xF0F0F0F0u, lo = (w[d] << 4) & 0xF0F0F0F0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[8 * d + 2 * i] = (float)(int8_t)((lo >> (8 * i)) & 255u);
+      f[8 * d + 2 * i + 1] = (float)(int8_t)((hi >> (8 * i)) & 255u);
+    }
+  }
+}
+
+// 8 of a run's 16 magnitudes (columns 8h .. 8h + 7 of a row): bfp8's 8 bytes, bfp4's 4 bytes (16 q as above)
+__device__ inline void magnitudes8(const uint2& m, float (&f)[8]) {
+  const uint32_t w[2] = {m.x, m.y};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = (float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 255u);
+}
+__device__ inline void magnitudes8(const uint32_t& m, float (&f)[8]) {
+  const uint32_t hi = m & 0xF0F0F0F0u, lo = (m << 4) & 0xF0F0F0F0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = (float)(int8_t)((lo >> (8 * i)) & 255u);
+    f[2 * i + 1] = (float)(int8_t)((hi >> (8 * i)) & 255u);
+  }
+}
+
+// N values of a run of a block float as bf16, two a word (value 2i low, 2i + 1 high), exactly: f holds q (bfp8) or
+// 16 q (bfp4, so both scale by 2^(top - 133)). q times a normal power of 2 is exact in fp32 (at most 7 significant
+// bits) and its upper half is its bf16; a scale below fp32's normals (top < 7) takes bfp_value_bf16's integer path.
+template <int N>
+__device__ inline void bfp_run_bf16(const float (&f)[N], uint32_t top, uint32_t (&w)[N / 2]) {
+  if (top >= 7) {
+    const float sc = __uint_as_float((top - 6) << 23);
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i)
+      w[i] = __builtin_amdgcn_perm(__float_as_uint(f[2 * i + 1] * sc), __float_as_uint(f[2 * i] * sc), 0x07060302u);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) w[i] = bfp_value_bf16((int32_t)f[2 * i], top) | (bfp_value_bf16((int32_t)f[2 * i + 1], top) << 16);
+  }
+}
+
+// A KV cache in a block float, [2 kv_heads][cache_len][head_dim] in one buffer: each row's magnitudes (head_dim bytes
+// of two's-complement q for bfp8; head_dim / 2 for bfp4, values 2i and 2i + 1 in a byte's low and high nibble), all
+// rows, then each row's head_dim / 16 exponents (a byte a run of 16), all rows.
+__host__ __device__ inline int64_t kv_mant_row(int fmt, int hd) { return fmt == FH_BFP4 ? hd / 2 : hd; }
+__host__ __device__ inline int64_t kv_exps_at(int fmt, int kv_heads, int64_t cache_len, int hd) {
+  return 2 * (int64_t)kv_heads * cache_len * kv_mant_row(fmt, hd);
+}
+
 // ---- wave64 reductions ------------------------------------------------------------------------------------------
 
 // Sum V values held by every lane over the wave's 64 lanes, transposing as it goes: at each lane bit (32 down to 1)

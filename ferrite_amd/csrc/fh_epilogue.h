@@ -22,7 +22,7 @@ struct MatArgs {
   int split;
   int heads, kv_heads, head_dim;
   const float* cos_tab; const float* sin_tab; const int32_t* places; const int32_t* cache_rows;
-  void* cache; int cache_bf16; int64_t cache_len;
+  void* cache; int cache_fmt; int64_t cache_len; uint8_t* cache_exps;  // (cache_exps: a block float's exponents)
   int2* argmax_parts;
   fh_program prog;          // FH_EP_PROGRAM
 };
@@ -34,38 +34,42 @@ __device__ inline void store_out(void* y, int bf16, int64_t at, float v) {
   else ((float*)y)[at] = v;
 }
 
-// the 16 magnitudes of a run's row as floats: bfp8's 16 bytes are the signed q; bfp4's 8 bytes give 16 q (the 16 is
-// folded into the scale: q * 2^(e - 129) = 16 q * 2^(e - 133))
-__device__ inline void magnitudes(const uint4& m, float (&f)[16]) {
-  const uint32_t w[4] = {m.x, m.y, m.z, m.w};
-#pragma unroll
-  for (int j = 0; j < 16; ++j) f[j] = (float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 255u);
-}
-__device__ inline void magnitudes(const uint2& m, float (&f)[16]) {
-  const uint32_t w[2] = {m.x, m.y};
-#pragma unroll
-  for (int d = 0; d < 2; ++d) {
-    const uint32_t hi = w[d] & 0xF0F0F0F0u, lo = (w[d] << 4) & 0xF0F0F0F0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[8 * d + 2 * i] = (float)(int8_t)((lo >> (8 * i)) & 255u);
-      f[8 * d + 2 * i + 1] = (float)(int8_t)((hi >> (8 * i)) & 255u);
-    }
+// A key or value pair into the cache: x0 at column d of cache row `row` (rows counted over all 2 kv_heads planes),
+// x1 at d + head_dim / 2. A block-float cache rounds bf16(x) (nearest even) run by run as fh_bfp_pack does
+// (ferrite/compiler.py:1638-1714, put_kernel): the 16 lanes lane & ~15 .. (lane & ~15) + 15 hold a run's 16 columns,
+// in order (j = lane & 15), and all of them must be here; the run's exponent is their largest.
+__device__ inline void cache_put(const MatArgs& a, int64_t row, int d, int d1, int j, float x0, float x1) {
+  const int hd = a.head_dim;
+  if (a.cache_fmt == FH_F32 || a.cache_fmt == FH_BF16) {
+    store_out(a.cache, a.cache_fmt == FH_BF16, row * hd + d, x0);
+    store_out(a.cache, a.cache_fmt == FH_BF16, row * hd + d1, x1);
+    return;
   }
-}
-
-// 8 of a run's 16 magnitudes (columns 8h .. 8h + 7 of a row): bfp8's 8 bytes, bfp4's 4 bytes (16 q as above)
-__device__ inline void magnitudes8(const uint2& m, float (&f)[8]) {
-  const uint32_t w[2] = {m.x, m.y};
+  const bool four = a.cache_fmt == FH_BFP4;
+  const uint32_t b0 = bf16_rne_f(x0), b1 = bf16_rne_f(x1);
+  uint32_t t0 = (b0 >> 7) & 255u, t1 = (b1 >> 7) & 255u;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) f[j] = (float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 255u);
-}
-__device__ inline void magnitudes8(const uint32_t& m, float (&f)[8]) {
-  const uint32_t hi = m & 0xF0F0F0F0u, lo = (m << 4) & 0xF0F0F0F0u;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = (float)(int8_t)((lo >> (8 * i)) & 255u);
-    f[2 * i + 1] = (float)(int8_t)((hi >> (8 * i)) & 255u);
+  for (int m = 8; m >= 1; m >>= 1) {
+    t0 = max(t0, (uint32_t)__shfl_xor((int)t0, m, 64));
+    t1 = max(t1, (uint32_t)__shfl_xor((int)t1, m, 64));
+  }
+  int q0 = (int)bfp_magnitude(b0, t0, four), q1 = (int)bfp_magnitude(b1, t1, four);
+  if (b0 >> 15) q0 = -q0;
+  if (b1 >> 15) q1 = -q1;
+  uint8_t* mant = (uint8_t*)a.cache;
+  if (four) {  // a byte holds columns 2i (low nibble) and 2i + 1
+    const int o0 = __shfl_xor(q0, 1, 64), o1 = __shfl_xor(q1, 1, 64);
+    if (!(j & 1)) {
+      mant[row * (hd / 2) + d / 2] = (uint8_t)((q0 & 15) | ((o0 & 15) << 4));
+      mant[row * (hd / 2) + d1 / 2] = (uint8_t)((q1 & 15) | ((o1 & 15) << 4));
+    }
+  } else {
+    mant[row * hd + d] = (uint8_t)q0;
+    mant[row * hd + d1] = (uint8_t)q1;
+  }
+  if (j == 0) {
+    a.cache_exps[row * (hd / 16) + d / 16] = (uint8_t)t0;
+    a.cache_exps[row * (hd / 16) + d1 / 16] = (uint8_t)t1;
   }
 }
 
@@ -121,12 +125,13 @@ inline int epilogue_args(const char* who, const fh_epilogue* ep, int64_t K, int6
           return bad(FH_EINVAL, "FH_EP_ROPE_KV needs N = (heads + 2 kv_heads) * head_dim, head_dim a multiple of 32");
         if (!ep->cos_tab || !ep->sin_tab || !ep->places || !ep->cache_rows || !ep->cache || ep->cache_len < 1)
           return bad(FH_EINVAL, "FH_EP_ROPE_KV needs tables, places, cache rows and a cache");
-        if (ep->cache_dtype != FH_F32 && ep->cache_dtype != FH_BF16) return bad(FH_EUNSUP, "cache is FH_F32 or FH_BF16");
+        if (ep->cache_dtype < FH_F32 || ep->cache_dtype > FH_BFP4) return bad(FH_EUNSUP, "cache is FH_F32, FH_BF16, FH_BFP8 or FH_BFP4");
         if (y_dtype != FH_F32) return bad(FH_EUNSUP, "FH_EP_ROPE_KV writes q in fp32");
         a.P = 2; a.pair_half = hd / 32; out_cols = (int64_t)ep->heads * hd;
         a.heads = ep->heads; a.kv_heads = ep->kv_heads; a.head_dim = hd;
         a.cos_tab = ep->cos_tab; a.sin_tab = ep->sin_tab; a.places = ep->places; a.cache_rows = ep->cache_rows;
-        a.cache = ep->cache; a.cache_bf16 = ep->cache_dtype == FH_BF16; a.cache_len = ep->cache_len;
+        a.cache = ep->cache; a.cache_fmt = ep->cache_dtype; a.cache_len = ep->cache_len;
+        a.cache_exps = (uint8_t*)ep->cache + kv_exps_at(ep->cache_dtype, ep->kv_heads, ep->cache_len, hd);
         break;
       }
       case FH_EP_PROGRAM:

@@ -282,9 +282,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
           q[d] = x0; q[d1] = x1;
         } else {
           const int ch = h - a.heads;
-          const int64_t at = ((int64_t)ch * a.cache_len + a.cache_rows[m]) * hd;
-          store_out(a.cache, a.cache_bf16, at + d, x0);
-          store_out(a.cache, a.cache_bf16, at + d1, x1);
+          cache_put(a, (int64_t)ch * a.cache_len + a.cache_rows[m], d, d1, j, x0, x1);
         }
       }
     }

@@ -198,9 +198,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
         q[d] = x0; q[d1] = x1;
       } else {  // keys' heads then values' heads, each at the row's cache row
         const int ch = h - a.heads;  // 0 .. 2 kv_heads - 1
-        const int64_t at = ((int64_t)ch * a.cache_len + a.cache_rows[b]) * hd;
-        store_out(a.cache, a.cache_bf16, at + d, x0);
-        store_out(a.cache, a.cache_bf16, at + d1, x1);
+        cache_put(a, (int64_t)ch * a.cache_len + a.cache_rows[b], d, d1, j, x0, x1);
       }
     }
   }

@@ -9,7 +9,8 @@
 // accumulated transposed too, O^T += V^T P^T, with P^T taken straight from the score registers: the order of the keys
 // inside a 16-key step does not change the sum, so V^T is read from LDS in the order the score layout holds them.
 // q, k, v go to bf16 for the matrix cores (as ferrite's chip holds them); scores, softmax and sums are fp32. Masked
-// scores are -1e30 (the reference adds -1e9; either leaves exp() at 0). Query tiles are issued longest first.
+// scores are -1e30 (the reference adds -1e9; either leaves exp() at 0). Query tiles are issued longest first. A
+// block-float cache's runs are decoded exactly into the bf16 tiles (their values are bf16 values).
 #include <math.h>
 #include "fh_common.h"
 
@@ -24,7 +25,7 @@ constexpr float PA_MASKED = -1e30f;
 
 struct PrefArgs {
   const float* q; int64_t ldq;
-  const void* cache; int64_t cache_len;
+  const void* cache; int64_t cache_len; const uint8_t* cache_exps;
   int T, heads, kv_heads; float scale;
   int64_t p0, slot_row;
   void* o; int64_t ldo; int o_bf16;
@@ -32,7 +33,27 @@ struct PrefArgs {
 
 __device__ inline uint32_t pack2_rne(float lo, float hi) { return bf16_rne_f(lo) | (bf16_rne_f(hi) << 16); }
 
-template <int HD, bool CBF16>
+// the 8 values c .. c + 7 (c a multiple of 8) of cache row `row` (rows counted over all 2 kv_heads planes) as bf16:
+// fp32 rounded to nearest even, bf16 as it is, a block float's exactly
+template <int HD, int CF>
+__device__ inline uint4 cache_bf16x8(const PrefArgs& a, int64_t row, int c) {
+  if constexpr (CF == FH_BF16) {
+    return *(const uint4*)((const uint16_t*)a.cache + row * HD + c);
+  } else if constexpr (CF == FH_F32) {
+    const float* p = (const float*)a.cache + row * HD + c;
+    const float4 u = *(const float4*)p, v = *(const float4*)(p + 4);
+    return make_uint4(pack2_rne(u.x, u.y), pack2_rne(u.z, u.w), pack2_rne(v.x, v.y), pack2_rne(v.z, v.w));
+  } else {
+    float f[8];
+    uint32_t w[4];
+    if constexpr (CF == FH_BFP8) magnitudes8(*(const uint2*)((const uint8_t*)a.cache + row * HD + c), f);
+    else magnitudes8(*(const uint32_t*)((const uint8_t*)a.cache + row * (HD / 2) + c / 2), f);
+    bfp_run_bf16<8>(f, a.cache_exps[row * (HD / 16) + c / 16], w);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <int HD, int CF>
 __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
   constexpr int KLD = HD + 8;        // K tile row in LDS (bf16): 16-byte aligned, banks spread
   constexpr int VLD = PA_BK + 8;     // V^T tile row (bf16)
@@ -70,9 +91,8 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
     for (int r = 0; r < 16; ++r) acc[d][r] = 0.f;
   float m = PA_MASKED, l = 0.f;
 
-  const size_t esz = CBF16 ? 2 : 4;
-  const char* kbase = (const char*)a.cache + ((int64_t)kvh * a.cache_len + a.slot_row) * HD * esz;
-  const char* vbase = (const char*)a.cache + ((int64_t)(a.kv_heads + kvh) * a.cache_len + a.slot_row) * HD * esz;
+  const int64_t krow = (int64_t)kvh * a.cache_len + a.slot_row;
+  const int64_t vrow = (int64_t)(a.kv_heads + kvh) * a.cache_len + a.slot_row;
 
   for (int kt = 0; kt < nkt; ++kt) {
     const int64_t k0 = (int64_t)kt * PA_BK;
@@ -81,14 +101,7 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
     for (int i = t; i < PA_BK * HD / 8; i += 256) {
       const int r = i / (HD / 8), c = (i % (HD / 8)) * 8;
       const int64_t key = min(k0 + r, last_key);
-      uint4 w;
-      if (CBF16) {
-        w = *(const uint4*)(kbase + (key * HD + c) * 2);
-      } else {
-        const float4 u = *(const float4*)(kbase + (key * HD + c) * 4), v = *(const float4*)(kbase + (key * HD + c + 4) * 4);
-        w = make_uint4(pack2_rne(u.x, u.y), pack2_rne(u.z, u.w), pack2_rne(v.x, v.y), pack2_rne(v.z, v.w));
-      }
-      *(uint4*)(Ks + r * KLD + c) = w;
+      *(uint4*)(Ks + r * KLD + c) = cache_bf16x8<HD, CF>(a, krow + key, c);
     }
     // V^T tile: a thread 4 keys x 8 dimensions, written as 8 rows of 4 keys
     for (int i = t; i < (PA_BK / 4) * (HD / 8); i += 256) {
@@ -97,13 +110,8 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int64_t key = min(k0 + 4 * kq + j, last_key);
-        if (CBF16) {
-          const uint4 w = *(const uint4*)(vbase + (key * HD + 8 * dg) * 2);
-          lo[j][0] = w.x; lo[j][1] = w.y; lo[j][2] = w.z; lo[j][3] = w.w;
-        } else {
-          const float4 u = *(const float4*)(vbase + (key * HD + 8 * dg) * 4), v = *(const float4*)(vbase + (key * HD + 8 * dg + 4) * 4);
-          lo[j][0] = pack2_rne(u.x, u.y); lo[j][1] = pack2_rne(u.z, u.w); lo[j][2] = pack2_rne(v.x, v.y); lo[j][3] = pack2_rne(v.z, v.w);
-        }
+        const uint4 w = cache_bf16x8<HD, CF>(a, vrow + key, 8 * dg);
+        lo[j][0] = w.x; lo[j][1] = w.y; lo[j][2] = w.z; lo[j][3] = w.w;
       }
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
@@ -215,6 +223,16 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(const float* x, int64_t l
   }
 }
 
+template <int HD>
+static void launch_prefill(int cf, dim3 g, dim3 b, hipStream_t s, const PrefArgs& a) {
+  switch (cf) {
+    case FH_F32: hipLaunchKernelGGL((attention_prefill_kernel<HD, FH_F32>), g, b, 0, s, a); break;
+    case FH_BF16: hipLaunchKernelGGL((attention_prefill_kernel<HD, FH_BF16>), g, b, 0, s, a); break;
+    case FH_BFP8: hipLaunchKernelGGL((attention_prefill_kernel<HD, FH_BFP8>), g, b, 0, s, a); break;
+    default: hipLaunchKernelGGL((attention_prefill_kernel<HD, FH_BFP4>), g, b, 0, s, a); break;
+  }
+}
+
 }  // namespace fh
 
 using namespace fh;
@@ -225,7 +243,8 @@ extern "C" int fh_attention_prefill(const float* q, int64_t ldq, const void* cac
   if (!q || !cache || !o) return fail(FH_EINVAL, "fh_attention_prefill: null pointer");
   if (T < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads) return fail(FH_EINVAL, "fh_attention_prefill: need T >= 1, heads a multiple of kv_heads");
   if (head_dim != 64 && head_dim != 128) return fail(FH_EUNSUP, "fh_attention_prefill: head_dim 64 or 128");
-  if (cache_dtype != FH_F32 && cache_dtype != FH_BF16) return fail(FH_EUNSUP, "fh_attention_prefill: cache is FH_F32 or FH_BF16");
+  if (cache_dtype < FH_F32 || cache_dtype > FH_BFP4)
+    return fail(FH_EUNSUP, "fh_attention_prefill: cache is FH_F32, FH_BF16, FH_BFP8 or FH_BFP4");
   if (o_dtype != FH_F32 && o_dtype != FH_BF16) return fail(FH_EINVAL, "fh_attention_prefill: o is FH_F32 or FH_BF16");
   if (ldq < (int64_t)heads * head_dim || ldo < (int64_t)heads * head_dim || ldq % 4 || ldo % 4)
     return fail(FH_EINVAL, "fh_attention_prefill: ldq and ldo at least heads * head_dim, multiples of 4");
@@ -233,18 +252,13 @@ extern "C" int fh_attention_prefill(const float* q, int64_t ldq, const void* cac
     return fail(FH_EINVAL, "fh_attention_prefill: the rows' keys (slot_row .. slot_row + p0 + T - 1) must lie in the cache");
   PrefArgs a = {};
   a.q = q; a.ldq = ldq; a.cache = cache; a.cache_len = cache_len;
+  a.cache_exps = (const uint8_t*)cache + kv_exps_at(cache_dtype, kv_heads, cache_len, head_dim);
   a.T = T; a.heads = heads; a.kv_heads = kv_heads; a.scale = 1.0f / sqrtf((float)head_dim);
   a.p0 = p0; a.slot_row = slot_row; a.o = o; a.ldo = ldo; a.o_bf16 = o_dtype == FH_BF16;
   const dim3 g((T + PA_BQ - 1) / PA_BQ, heads), b(256);
   hipStream_t s = as_stream(stream);
-  const bool bf = cache_dtype == FH_BF16;
-  if (head_dim == 128) {
-    if (bf) hipLaunchKernelGGL((attention_prefill_kernel<128, true>), g, b, 0, s, a);
-    else hipLaunchKernelGGL((attention_prefill_kernel<128, false>), g, b, 0, s, a);
-  } else {
-    if (bf) hipLaunchKernelGGL((attention_prefill_kernel<64, true>), g, b, 0, s, a);
-    else hipLaunchKernelGGL((attention_prefill_kernel<64, false>), g, b, 0, s, a);
-  }
+  if (head_dim == 128) launch_prefill<128>(cache_dtype, g, b, s, a);
+  else launch_prefill<64>(cache_dtype, g, b, s, a);
   return check_launch("fh_attention_prefill");
 }
 

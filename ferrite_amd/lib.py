@@ -50,6 +50,7 @@ SIGNATURES = {
   "fh_gemm_bfp": ([P, I, L, L, L, L, P, P, I, ctypes.POINTER(Epilogue), P, I, L, P], I),
   "fh_embed_rows": ([P, I, L, L, P, I, P, P, P], I),
   "fh_attention_workspace_bytes": ([I, I, I, L], S),
+  "fh_kv_cache_bytes": ([I, I, L, I], S),
   "fh_attention_decode": ([P, P, I, L, I, I, I, I, P, P, L, P, P, S, P], I),
   "fh_attention_prefill": ([P, L, P, I, L, I, I, I, I, L, L, P, I, L, P], I),
   "fh_rms_rows": ([P, L, L, L, P, ctypes.c_float, I, P, I, L, P], I),

@@ -124,8 +124,10 @@ class Decoder:
     # the KV cache: a block's keys' heads then values', `slots` sequences' rows side by side (models/llama.py:506-514)
     self.slots = slots or 1
     self.part = context  # rows a sequence
-    self.kv_dtype = {"bf16": torch.bfloat16, "fp32": torch.float32}[kv]
-    self.cache = [torch.zeros(2 * c.kv, self.slots * context, hd, dtype=self.kv_dtype, device=self.device) for _ in range(c.layers)]
+    # (bfp8 / bfp4: a block-float cache, each run of 16 of a row rounded as the qkv epilogue puts it; llama.py:127-128)
+    if kv not in ("fp32", "bf16", "bfp8", "bfp4"): raise ValueError(f"kv cache: fp32, bf16, bfp8 or bfp4, not {kv}")
+    self.kv = kv
+    self.cache = [ops.kv_cache(2 * c.kv, self.slots * context, hd, kv, self.device) for _ in range(c.layers)]
     # a step's buffers, fixed so a step replays as a graph
     B = batch
     z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.device)
@@ -158,6 +160,10 @@ class Decoder:
     self.first.copy_(slots * self.part)
     self.rows.copy_(slots * self.part + places)
 
+  def _cache(self, l):
+    data, dtype, length = ops.cache_fields(self.cache[l])
+    return dict(cache=data, cache_dtype=dtype, cache_len=length)
+
   def _step(self):
     if self.mm is ops.gemm: return self._step_rows()
     c, B, hd = self.c, self.batch, self.hd
@@ -165,8 +171,7 @@ class Decoder:
     for l, L in enumerate(self.layers):
       ep = ops.epilogue(lib.EP_ROPE_KV, norm_w=L.norm1, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered),
                         heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
-                        places=self.places, cache_rows=self.rows, cache=self.cache[l],
-                        cache_dtype=lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"], cache_len=self.cache[l].shape[1])
+                        places=self.places, cache_rows=self.rows, **self._cache(l))
       ops.gemv(self.x, L.qkv, ep, out=self.q)
       ops.attention_decode(self.q, self.cache[l], c.heads, c.kv, hd, self.places, self.first, self.context, self.ws, o=self.att)
       ep = ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq)
@@ -196,11 +201,10 @@ class Decoder:
     c, B, hd = self.c, self.batch, self.hd
     nw = self._norm_weights()
     ops.embed_rows(self.embed, self.ids, self.x, self.ssq)
-    cache_dtype = lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"]
     rs = dict(ssq_in=self.ssq, eps=c.eps)  # rows that hold x w: 1/rms only
     for l, L in enumerate(self.layers):
       rope = dict(heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin, places=self.places,
-                  cache_rows=self.rows, cache=self.cache[l], cache_dtype=cache_dtype, cache_len=self.cache[l].shape[1])
+                  cache_rows=self.rows, **self._cache(l))
       if l == 0:
         ops.rms_rows(self.x, L.norm1, c.eps, c.centered, out=self.xn)
         ops.gemm(self.xn, L.qkv, ops.epilogue(lib.EP_ROPE_KV, **rope), out=self.q)
@@ -248,15 +252,13 @@ class Decoder:
     ids_t.copy_(torch.as_tensor(ids, dtype=torch.int32))
     places.copy_(torch.arange(p0, p0 + T, dtype=torch.int32))
     rows.copy_(places + slot * self.part)
-    cache_dtype = lib.DTYPES["bf16" if self.kv_dtype == torch.bfloat16 else "fp32"]
     ops.embed_rows(self.embed, ids_t, x, ssq)
     # (each RMSNorm a pass of its own here: at 2048 rows the tiled kernel's per-tile sums of the rows' squares cost
     # more than fh_rms_rows; the batched decode takes the residual epilogues' scaled copies instead)
     for l, L in enumerate(self.layers):
       ops.rms_rows(x, L.norm1, c.eps, c.centered, out=xn)
       ep = ops.epilogue(lib.EP_ROPE_KV, heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
-                        places=places, cache_rows=rows, cache=self.cache[l], cache_dtype=cache_dtype,
-                        cache_len=self.cache[l].shape[1])
+                        places=places, cache_rows=rows, **self._cache(l))
       ops.gemm(xn, L.qkv, ep, out=q)
       ops.attention_prefill(q, self.cache[l], c.heads, c.kv, hd, p0, slot * self.part, o=att)
       ops.gemm(att, L.o, ops.epilogue(lib.EP_RESIDUAL, residual=x), out=x)

@@ -109,17 +109,62 @@ def embed_rows(table, ids, x=None, ssq=None):
   return x, ssq
 
 
+@dataclass
+class BfpCache:
+  """A KV cache [planes = 2 kv][length][head_dim] in a block float (bfp8 or bfp4; models/llama.py:127-128): one uint8
+  buffer in fh_kv_cache_bytes' layout, every row's magnitudes then every row's exponents. Zero bytes: zeros."""
+  data: torch.Tensor
+  fmt: str
+  planes: int
+  length: int
+  head_dim: int
+
+  @property
+  def shape(self): return (self.planes, self.length, self.head_dim)
+
+  @property
+  def dtype(self): return self.fmt
+
+  def zero_(self):
+    self.data.zero_()
+    return self
+
+  def copy_(self, other):
+    if other.shape != self.shape or other.fmt != self.fmt: raise ValueError("BfpCache.copy_: another shape or format")
+    self.data.copy_(other.data)
+    return self
+
+
+def kv_cache(planes, length, head_dim, fmt="bf16", device="cuda"):
+  """A KV cache of zeros [planes][length][head_dim]: a torch tensor for fp32 and bf16, a BfpCache for bfp8 and bfp4."""
+  if fmt in ("fp32", "bf16"):
+    return torch.zeros(planes, length, head_dim, dtype=torch.float32 if fmt == "fp32" else torch.bfloat16, device=device)
+  if planes % 2: raise ValueError("kv_cache: keys' planes then values', an even count")
+  n = lib.load().fh_kv_cache_bytes(lib.DTYPES[fmt], planes // 2, length, head_dim)
+  if not n: raise ValueError(f"kv_cache: no {fmt} cache of head_dim {head_dim}")
+  return BfpCache(torch.zeros(n, dtype=torch.uint8, device=device), fmt, planes, length, head_dim)
+
+
+def cache_fields(cache):
+  """The fh_epilogue / attention arguments of a cache: (tensor, cache_dtype, cache_len)."""
+  if isinstance(cache, BfpCache): return cache.data, lib.DTYPES[cache.fmt], cache.length
+  if cache.dtype not in _TORCH or cache.dim() != 3: raise ValueError("a KV cache is [2 kv][len][hd], fp32 or bf16, or a BfpCache")
+  return cache, _TORCH[cache.dtype], cache.shape[1]
+
+
 def attention_workspace(batch, heads, head_dim, max_context, device="cuda"):
   n = lib.load().fh_attention_workspace_bytes(batch, heads, head_dim, max_context)
   return torch.zeros(max(n, 256), dtype=torch.uint8, device=device)
 
 
 def attention_decode(q, cache, heads, kv_heads, head_dim, places, first_row, max_context, workspace, o=None):
-  """softmax(q k^T / sqrt(hd)) v over each row's cache rows (fh_attention_decode). cache [2 kv][len][hd]."""
-  _dev(q, cache, places, first_row)
+  """softmax(q k^T / sqrt(hd)) v over each row's cache rows (fh_attention_decode). cache [2 kv][len][hd] (fp32, bf16 or
+  a BfpCache)."""
+  data, dtype, length = cache_fields(cache)
+  _dev(q, data, places, first_row)
   batch = q.shape[0]
   if o is None: o = torch.empty_like(q)
-  lib.call("fh_attention_decode", _ptr(q), _ptr(cache), _TORCH[cache.dtype], cache.shape[1], batch, heads, kv_heads,
+  lib.call("fh_attention_decode", _ptr(q), _ptr(data), dtype, length, batch, heads, kv_heads,
            head_dim, _ptr(places), _ptr(first_row), max_context, _ptr(o), _ptr(workspace), workspace.numel(), _stream())
   return o
 
@@ -127,11 +172,12 @@ def attention_decode(q, cache, heads, kv_heads, head_dim, places, first_row, max
 def attention_prefill(q, cache, heads, kv_heads, head_dim, p0, slot_row, o=None, out_dtype=torch.float32):
   """A prompt's causal attention (fh_attention_prefill): q [T][heads*hd] at places p0 .. p0 + T - 1 of the sequence
   whose cache rows start at slot_row; cache [2 kv][len][hd]."""
-  _dev(q, cache)
+  data, dtype, length = cache_fields(cache)
+  _dev(q, data)
   T = q.shape[0]
   if o is None: o = torch.empty(T, heads * head_dim, dtype=out_dtype, device=q.device)
   _dev(o)
-  lib.call("fh_attention_prefill", _ptr(q), q.stride(0), _ptr(cache), _TORCH[cache.dtype], cache.shape[1], T, heads,
+  lib.call("fh_attention_prefill", _ptr(q), q.stride(0), _ptr(data), dtype, length, T, heads,
            kv_heads, head_dim, p0, slot_row, _ptr(o), _TORCH[o.dtype], o.stride(0), _stream())
   return o
 

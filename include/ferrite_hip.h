@@ -127,8 +127,10 @@ typedef struct fh_epilogue {
   const float* sin_tab;     /* [places][head_dim] */
   const int32_t* places;    /* [batch]: each row's place (its rotary row) */
   const int32_t* cache_rows;/* [batch]: the cache row each row's k and v go to (its slot's first row + place) */
-  void* cache;              /* [2*kv_heads][cache_len][head_dim]: keys' heads then values', fp32 or bf16 */
-  int cache_dtype;
+  void* cache;              /* [2*kv_heads][cache_len][head_dim]: keys' heads then values' (fh_kv_cache_bytes) */
+  int cache_dtype;          /* FH_F32, FH_BF16, or a block float: FH_BFP8 or FH_BFP4, each run of 16 of a row
+                             * rounded from bf16(k or v) as fh_bfp_pack rounds it (Tensor.put into a block-float
+                             * cache, ferrite/compiler.py:1638-1714) */
   int64_t cache_len;
   /* FH_EP_STORE: each row's largest value of each run of 16 columns and its column (the first of equals), as
    * (float, int32) pairs [batch][N/16], for fh_argmax_parts: greedy decoding's pick without a second pass over y */
@@ -179,6 +181,14 @@ int fh_embed_rows(const void* table, int table_dtype, int64_t vocab, int64_t dim
  * by exp-weights (ferrite/compiler.py:1138-1145); a context of one chunk writes o directly. The workspace holds no
  * state between calls (what a call does not write, it does not read). */
 size_t fh_attention_workspace_bytes(int batch, int heads, int head_dim, int64_t max_context);
+/* A KV cache's bytes: [2*kv_heads][cache_len][head_dim] of fp32 or bf16; or a block float (models/llama.py:127-128,
+ * a cache in bfp8 or bfp4), one buffer: every row's magnitudes (head_dim bytes of two's-complement q for FH_BFP8;
+ * head_dim / 2 for FH_BFP4, columns 2i and 2i + 1 in a byte's low and high nibble), rows in order, then every row's
+ * head_dim / 16 exponents (a byte a run of 16 columns), rows in order; the values are q * 2^(e - 133) (FH_BFP8),
+ * q * 2^(e - 129) (FH_BFP4). All zero bytes are a cache of zeros. 0 for bad arguments (head_dim not a multiple of 32,
+ * an unknown dtype). Attention decodes a block float's runs to bf16 exactly: its results are a bf16 cache's holding
+ * the same values. No counterpart in the reference as a function (its cache is a Tensor of that dtype). */
+size_t fh_kv_cache_bytes(int cache_dtype, int kv_heads, int64_t cache_len, int head_dim);
 int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch, int heads,
                         int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row, int64_t max_context,
                         float* o, void* workspace, size_t ws_bytes, void* stream);

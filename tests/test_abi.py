@@ -38,3 +38,8 @@ def test_errors_without_gpu_work():
   with pytest.raises(ValueError):
     lib.call("fh_gemv_bfp", None, lib.F32, 16, 1, 16, 16, None, None, lib.BFP8, None, None, lib.F32, 16, None)
   assert lib.load().fh_version().decode().endswith("gfx950")
+  # a KV cache's bytes: fp32 / bf16 elements; a block float's magnitudes then a byte a run of 16 (2 kv heads, 10 rows)
+  kb = lib.load().fh_kv_cache_bytes
+  assert kb(lib.F32, 2, 10, 64) == 4 * 10 * 64 * 4 and kb(lib.BF16, 2, 10, 64) == 4 * 10 * 64 * 2
+  assert kb(lib.BFP8, 2, 10, 128) == 4 * 10 * (128 + 8) and kb(lib.BFP4, 2, 10, 128) == 4 * 10 * (64 + 8)
+  assert kb(lib.BFP8, 2, 10, 48) == 0 and kb(7, 2, 10, 64) == 0
