@@ -1,31 +1,37 @@
-// Decode attention over a KV cache, flash-decoding style, in two kernels. The first: a workgroup takes a chunk of 64
-// cache rows of one batch row for one key head, with a wave for each query head that reads it (grouped-query: query
-// head h reads key head h / (heads / kv_heads)). Its threads load the chunk's keys and values into LDS once (each
-// byte of the cache read once from HBM; every load of the chunk and of q in flight together, one memory round trip);
-// each wave then scores the 64 rows against its head's q (a lane a row), takes their largest score and sum of exps,
-// and accumulates p * v (a lane HD / 64 dimensions, four rows' p a broadcast read). A row whose keys fit one chunk
-// writes o directly; otherwise each chunk's (p v, max, sum) goes to the workspace, and the second kernel combines the
-// chunks of each (row, head): a thread a chunk's statistics and a dimension's values, all loaded in one round with the
-// row's place, one exp(max - the largest) a thread. A kernel boundary, not a fence, orders the two: on MI355X an
-// agent-scope release (an L2 write-back on each XCD) and a counter cost more than the ~1.4 us boundary. A row reads
-// only the cache rows its place reaches. A block-float cache (bfp8 or bfp4) is decoded into the same bf16 tiles as it
-// is loaded, exactly (a run's values are bf16 values), so its results are bit for bit a bf16 cache's of those values.
+// Decode attention over a KV cache, flash-decoding style, in two kernels. The first: a workgroup takes one key head
+// of one batch row, with a wave for each query head that reads it (grouped-query: query head h reads key head h /
+// (heads / kv_heads)), and walks chunks of 64 cache rows: split, split + S, split + 2S, ... where S workgroups share
+// the row's chunks (S sized so the whole grid is resident at once). Its threads stage each chunk's keys and values in
+// LDS (each byte of the cache read once from HBM) and issue the next chunk's loads into registers before the waves
+// compute on this one, so the loads of one chunk overlap the arithmetic of the one before. Each wave scores the 64
+// rows against its head's q (a lane a row; q read through the scalar unit, one address for the whole wave, where a
+// workgroup walks several chunks; where it takes one, q is staged in LDS with the chunk's loads instead), keeps a
+// running max and sum of exps across its chunks (online softmax), and accumulates p * v (a lane HD / 64 dimensions,
+// four rows' p a broadcast read). A row whose chunks all fall to one workgroup writes o directly; otherwise each
+// workgroup's (p v, max, sum) goes to the workspace, and the second kernel combines the S parts of each (row, head):
+// a thread a part's statistics and a dimension's values, all loaded in one round with the row's place, one exp(max -
+// the largest) a thread. A kernel boundary, not a fence, orders the two: on MI355X an agent-scope release (an L2
+// write-back on each XCD) and a counter cost more than the ~1.4 us boundary. A row reads only the cache rows its
+// place reaches. A block-float cache (bfp8 or bfp4) is decoded into the same bf16 tiles as it is staged, exactly (a
+// run's values are bf16 values), so its results are bit for bit a bf16 cache's of those values.
 #include <math.h>
+#include <algorithm>
 #include <type_traits>
 #include "fh_common.h"
 
 namespace fh {
 
-constexpr int ATT_CHUNK = 64;                // cache rows a workgroup (a lane a row)
+constexpr int ATT_CHUNK = 64;                // cache rows a chunk (a lane a row)
 constexpr int ATT_REP = 16;                  // query heads a key head, at most (a wave each)
 
 struct AttArgs {
   const float* q; const void* cache; int64_t cache_len; const uint8_t* cache_exps;
   int heads, kv_heads; float scale;
   const int32_t* places; const int32_t* first_row;
-  int max_chunks;
+  int max_chunks;       // the launch's context in chunks (a row reads at most this many)
+  int splits;           // S: workgroups a (row, key head), = gridDim.x
   float* o;
-  float* part;          // [batch][heads][max_chunks][hd + 2]: p v, then max, then sum
+  float* part;          // [batch][heads][splits][hd + 2]: p v, then max, then sum
 };
 
 // the row's cache rows, kept inside the cache and the launch's chunks whatever the places say
@@ -37,176 +43,189 @@ __device__ inline void row_range(const AttArgs& a, int b, int64_t& row0, int64_t
   length = length < 1 ? 1 : (length > room ? room : length);
 }
 
-// LDS a workgroup: keys and values [64][row + 16 bytes], the heads' q [rep][HD] fp32, their p [rep][64]
+// LDS a workgroup: keys and values [64][row + 16 bytes] (bf16, or fp32 for an fp32 cache), the heads' p [rep][64],
+// and where q is staged, the heads' q [rep][HD] fp32
 __host__ __device__ constexpr int att_row_bytes(int hd, int es) { return hd * es + 16; }
-static size_t att_lds(int hd, int es, int rep) {
-  return (size_t)2 * ATT_CHUNK * att_row_bytes(hd, es) + (size_t)rep * hd * 4 + (size_t)rep * ATT_CHUNK * 4;
+static size_t att_lds(int hd, int es, int rep, bool q_lds) {
+  return (size_t)2 * ATT_CHUNK * att_row_bytes(hd, es) + (size_t)rep * ATT_CHUNK * 4 + (q_lds ? (size_t)rep * hd * 4 : 0);
 }
 
+// A chunk's keys and values, a thread's share of one round (4 pieces of each; a piece is 16 bytes of an fp32 or bf16
+// row, or a run of 16 of a block float with its exponent byte): load() issues the round's loads into registers,
+// store() writes them into the LDS tiles (a block float's runs decoded to bf16). Rows past the chunk's n read its last
+// row (unused); pieces past the tile read its last piece again.
 template <int HD, int CF>
+struct ChunkLoader {
+  static constexpr bool BLOCK = CF == FH_BFP8 || CF == FH_BFP4;
+  static constexpr int ES = CF == FH_F32 ? 4 : 2;                 // bytes an element in LDS
+  static constexpr int RW = att_row_bytes(HD, ES);
+  static constexpr int PER_ROW = BLOCK ? HD / 16 : HD * ES / 16;   // pieces a row
+  static constexpr int PIECES = ATT_CHUNK * PER_ROW;
+  using Piece = typename std::conditional<CF == FH_BFP4, uint2, uint4>::type;
+  Piece kp[4], vp[4];
+  uint32_t kx[4], vx[4];
+
+  __device__ __forceinline__ void load(const AttArgs& a, int64_t krow, int64_t vrow, int n, int i0, int tid, int nthreads) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(i0 + u * nthreads + tid, PIECES - 1);
+      const int r = i / PER_ROW, pc = i % PER_ROW, rr = r < n ? r : n - 1;
+      if constexpr (BLOCK) {
+        kp[u] = ((const Piece*)a.cache)[(krow + rr) * PER_ROW + pc]; kx[u] = a.cache_exps[(krow + rr) * PER_ROW + pc];
+        vp[u] = ((const Piece*)a.cache)[(vrow + rr) * PER_ROW + pc]; vx[u] = a.cache_exps[(vrow + rr) * PER_ROW + pc];
+      } else {
+        kp[u] = *(const uint4*)((const char*)a.cache + (krow + rr) * (HD * ES) + 16 * pc);
+        vp[u] = *(const uint4*)((const char*)a.cache + (vrow + rr) * (HD * ES) + 16 * pc);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(char* ks, char* vs, int i0, int tid, int nthreads) const {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * nthreads + tid;
+      if (i >= PIECES) continue;
+      const int r = i / PER_ROW, pc = i % PER_ROW;
+      if constexpr (BLOCK) {
+        float f[16];
+        uint32_t w[8];
+        uint4* kd = (uint4*)(ks + r * RW + 32 * pc);
+        uint4* vd = (uint4*)(vs + r * RW + 32 * pc);
+        magnitudes(kp[u], f);
+        bfp_run_bf16<16>(f, kx[u], w);
+        kd[0] = make_uint4(w[0], w[1], w[2], w[3]); kd[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        magnitudes(vp[u], f);
+        bfp_run_bf16<16>(f, vx[u], w);
+        vd[0] = make_uint4(w[0], w[1], w[2], w[3]); vd[1] = make_uint4(w[4], w[5], w[6], w[7]);
+      } else {
+        *(uint4*)(ks + r * RW + 16 * pc) = make_uint4(kp[u].x, kp[u].y, kp[u].z, kp[u].w);
+        *(uint4*)(vs + r * RW + 16 * pc) = make_uint4(vp[u].x, vp[u].y, vp[u].z, vp[u].w);
+      }
+    }
+  }
+};
+
+template <int HD, int CF, bool QLDS>
 __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(AttArgs a) {
+  using Loader = ChunkLoader<HD, CF>;
   constexpr bool BF = CF != FH_F32;            // the tiles in bf16 (a bf16 or block-float cache)
   constexpr int DL = HD / 64;                  // dimensions a lane (p v, the combine)
-  constexpr int ES = BF ? 2 : 4;               // bytes an element in LDS
+  constexpr int ES = Loader::ES;
   constexpr int V16 = HD * ES / 16;            // 16-byte pieces a row in LDS
-  constexpr int RW = att_row_bytes(HD, ES);    // (16 more than the row: a lane's 16-byte reads of its own row spread
+  constexpr int RW = Loader::RW;               // (16 more than the row: a lane's 16-byte reads of its own row spread
                                                // over the banks)
   extern __shared__ __attribute__((aligned(16))) char att_smem[];
-  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, S = a.splits;
   const int rep = a.heads / a.kv_heads;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthreads = 64 * rep;
+  const int tid = threadIdx.x, lane = tid & 63, nthreads = 64 * rep;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = kvh * rep + wave;              // this wave's query head
   int64_t row0, length;
   row_range(a, b, row0, length);
   const int nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);
-  if (chunk >= nchunks) return;  // past the row's place
-  const int64_t c0 = (int64_t)chunk * ATT_CHUNK;
-  const int n = (int)(length - c0 < ATT_CHUNK ? length - c0 : ATT_CHUNK);  // rows of this chunk (>= 1)
+  if (split >= nchunks) return;  // no chunk of the row falls to this workgroup
+  const int parts = nchunks < S ? nchunks : S;  // workgroups with a share of the row
   char* ks = att_smem;
   char* vs = att_smem + ATT_CHUNK * RW;
-  float* qs = (float*)(att_smem + 2 * ATT_CHUNK * RW);
-  float* ps = qs + rep * HD + wave * ATT_CHUNK;  // this wave's p
+  float* ps = (float*)(att_smem + 2 * ATT_CHUNK * RW) + wave * ATT_CHUNK;  // this wave's p
+  float* qs = (float*)(att_smem + 2 * ATT_CHUNK * RW) + rep * ATT_CHUNK;   // (QLDS) the heads' q
+  // q: one address for the wave (scalar loads), or the wave's row of the staged q
+  const float* qh = QLDS ? qs + wave * HD : a.q + ((int64_t)b * a.heads + h) * HD;
+  const int64_t krow0 = (int64_t)kvh * a.cache_len + row0, vrow0 = (int64_t)(a.kv_heads + kvh) * a.cache_len + row0;
+  auto rows_of = [&](int c) { return (int)(length - (int64_t)c * ATT_CHUNK < ATT_CHUNK ? length - (int64_t)c * ATT_CHUNK : ATT_CHUNK); };
 
-  const float* qrow = a.q + ((int64_t)b * a.heads + (int64_t)kvh * rep) * HD;
-  if constexpr (CF == FH_F32 || CF == FH_BF16) {
-    // the chunk's keys and values into LDS, 16 bytes a thread a piece, and the heads' q: every load issued before any
-    // LDS store (rows past n read the last row, unused; pieces past the chunk read its last piece again)
-    constexpr int PIECES = ATT_CHUNK * V16;
-    const char* kb = (const char*)a.cache + ((int64_t)kvh * a.cache_len + row0 + c0) * HD * ES;
-    const char* vb = (const char*)a.cache + ((int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + c0) * HD * ES;
-    for (int i0 = 0; i0 < PIECES; i0 += 4 * nthreads) {
-      uint4 kp[4], vp[4];
-      float4 qp = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = min(i0 + u * nthreads + tid, PIECES - 1);
-        const int r = i / V16, pc = i % V16, rr = r < n ? r : n - 1;
-        kp[u] = *(const uint4*)(kb + (int64_t)rr * HD * ES + 16 * pc);
-        vp[u] = *(const uint4*)(vb + (int64_t)rr * HD * ES + 16 * pc);
-      }
-      if (i0 == 0) qp = *(const float4*)(qrow + 4 * min(tid, rep * HD / 4 - 1));  // (rep HD / 4 <= 16 HD / 4 <= 64 rep)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * nthreads + tid;
-        if (i < PIECES) {
-          *(uint4*)(ks + (i / V16) * RW + 16 * (i % V16)) = kp[u];
-          *(uint4*)(vs + (i / V16) * RW + 16 * (i % V16)) = vp[u];
-        }
-      }
-      if (i0 == 0 && tid < rep * HD / 4) *(float4*)(qs + 4 * tid) = qp;
-    }
-  } else {
-    // a block float: a thread a run of 16 (its magnitudes and exponent byte) a piece, decoded to bf16 into LDS
-    // (32 bytes), the same order of loads then stores
-    using Run = typename std::conditional<CF == FH_BFP8, uint4, uint2>::type;
-    constexpr int RUNS = HD / 16, PIECES = ATT_CHUNK * RUNS;
-    const int64_t kr = (int64_t)kvh * a.cache_len + row0 + c0, vr = (int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + c0;
-    const Run* km = (const Run*)a.cache + kr * RUNS;
-    const Run* vm = (const Run*)a.cache + vr * RUNS;
-    const uint8_t* ke = a.cache_exps + kr * RUNS;
-    const uint8_t* ve = a.cache_exps + vr * RUNS;
-    for (int i0 = 0; i0 < PIECES; i0 += 4 * nthreads) {
-      Run kp[4], vp[4];
-      uint32_t kx[4], vx[4];
-      float4 qp = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = min(i0 + u * nthreads + tid, PIECES - 1);
-        const int r = i / RUNS, pc = i % RUNS, rr = r < n ? r : n - 1;
-        kp[u] = km[rr * RUNS + pc]; kx[u] = ke[rr * RUNS + pc];
-        vp[u] = vm[rr * RUNS + pc]; vx[u] = ve[rr * RUNS + pc];
-      }
-      if (i0 == 0) qp = *(const float4*)(qrow + 4 * min(tid, rep * HD / 4 - 1));
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * nthreads + tid;
-        if (i < PIECES) {
-          float f[16];
-          uint32_t w[8];
-          uint4* kd = (uint4*)(ks + (i / RUNS) * RW + 32 * (i % RUNS));
-          uint4* vd = (uint4*)(vs + (i / RUNS) * RW + 32 * (i % RUNS));
-          magnitudes(kp[u], f);
-          bfp_run_bf16<16>(f, kx[u], w);
-          kd[0] = make_uint4(w[0], w[1], w[2], w[3]); kd[1] = make_uint4(w[4], w[5], w[6], w[7]);
-          magnitudes(vp[u], f);
-          bfp_run_bf16<16>(f, vx[u], w);
-          vd[0] = make_uint4(w[0], w[1], w[2], w[3]); vd[1] = make_uint4(w[4], w[5], w[6], w[7]);
-        }
-      }
-      if (i0 == 0 && tid < rep * HD / 4) *(float4*)(qs + 4 * tid) = qp;
-    }
+  Loader ld;
+  ld.load(a, krow0 + (int64_t)split * ATT_CHUNK, vrow0 + (int64_t)split * ATT_CHUNK, rows_of(split), 0, tid, nthreads);
+  if constexpr (QLDS) {  // q with the first chunk's loads (rep HD / 4 <= 16 HD / 4 <= 64 rep float4s: one each at most)
+    const float* qrow = a.q + ((int64_t)b * a.heads + (int64_t)kvh * rep) * HD;
+    const float4 qp = *(const float4*)(qrow + 4 * min(tid, rep * HD / 4 - 1));
+    if (tid < rep * HD / 4) *(float4*)(qs + 4 * tid) = qp;
   }
-  __syncthreads();
-
-  // the lane's row's score: its keys (from LDS) dotted with the head's q (an LDS broadcast)
-  const float* qh = qs + wave * HD;
-  float s2[2] = {0.f, 0.f};
-  const char* krow = ks + lane * RW;
-#pragma unroll
-  for (int p = 0; p < V16; ++p) {
-    const uint4 w4 = *(const uint4*)(krow + 16 * p);
-    const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
-    const float4 qa = *(const float4*)(qh + p * (16 / ES)), qb = BF ? *(const float4*)(qh + p * 8 + 4) : qa;
-    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (BF) {
-        s2[0] = fmaf(qv[2 * j], __uint_as_float(w[j] << 16), s2[0]);
-        s2[1] = fmaf(qv[2 * j + 1], __uint_as_float(w[j] & 0xFFFF0000u), s2[1]);
-      } else {
-        s2[j & 1] = fmaf(qv[j], __uint_as_float(w[j]), s2[j & 1]);
-      }
-    }
-  }
-  const bool valid = lane < n;
-  const float sc = valid ? (s2[0] + s2[1]) * a.scale : -INFINITY;
-  const float mx = wave_max(sc);
-  const float p = valid ? expf(sc - mx) : 0.f;
-  const float sm = wave_sum(p);
-  ps[lane] = p;
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the wave's p visible to all its lanes
-
-  // p v: a lane dimensions DL lane .. DL lane + DL - 1
-  float o[DL];
+  float m = -INFINITY, l = 0.f, o[DL];
 #pragma unroll
   for (int i = 0; i < DL; ++i) o[i] = 0.f;
-#pragma unroll 4
-  for (int t4 = 0; t4 < ATT_CHUNK / 4; ++t4) {
-    const float4 p4 = *(const float4*)(ps + 4 * t4);
-    const float pt[4] = {p4.x, p4.y, p4.z, p4.w};
+  for (int c = split; c < nchunks; c += S) {
+    const int n = rows_of(c);
+    const int64_t kr = krow0 + (int64_t)c * ATT_CHUNK, vr = vrow0 + (int64_t)c * ATT_CHUNK;
+    ld.store(ks, vs, 0, tid, nthreads);
+    for (int i0 = 4 * nthreads; i0 < Loader::PIECES; i0 += 4 * nthreads) {  // (tiles beyond a round a thread)
+      ld.load(a, kr, vr, n, i0, tid, nthreads);
+      ld.store(ks, vs, i0, tid, nthreads);
+    }
+    __syncthreads();
+    if (c + S < nchunks)  // the next chunk's first round in flight during this one's arithmetic
+      ld.load(a, kr + (int64_t)S * ATT_CHUNK, vr + (int64_t)S * ATT_CHUNK, rows_of(c + S), 0, tid, nthreads);
+
+    // the lane's row's score: its keys (from LDS) dotted with the head's q
+    float s2[2] = {0.f, 0.f};
+    const char* krow = ks + lane * RW;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const char* vr = vs + (4 * t4 + u) * RW + DL * ES * lane;
-      if constexpr (BF && DL == 2) {
-        const uint32_t w = *(const uint32_t*)vr;
-        o[0] = fmaf(pt[u], __uint_as_float(w << 16), o[0]);
-        o[1] = fmaf(pt[u], __uint_as_float(w & 0xFFFF0000u), o[1]);
-      } else {
+    for (int p = 0; p < V16; ++p) {
+      const uint4 w4 = *(const uint4*)(krow + 16 * p);
+      const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+      const float4 qa = *(const float4*)(qh + p * (16 / ES)), qb = BF ? *(const float4*)(qh + p * 8 + 4) : qa;
+      const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
-        for (int i = 0; i < DL; ++i) {
-          const float x = BF ? __uint_as_float((uint32_t)((const uint16_t*)vr)[i] << 16) : ((const float*)vr)[i];
-          o[i] = fmaf(pt[u], x, o[i]);
+      for (int j = 0; j < 4; ++j) {
+        if (BF) {
+          s2[0] = fmaf(qv[2 * j], __uint_as_float(w[j] << 16), s2[0]);
+          s2[1] = fmaf(qv[2 * j + 1], __uint_as_float(w[j] & 0xFFFF0000u), s2[1]);
+        } else {
+          s2[j & 1] = fmaf(qv[j], __uint_as_float(w[j]), s2[j & 1]);
         }
       }
     }
+    const bool valid = lane < n;
+    const float sc = valid ? (s2[0] + s2[1]) * a.scale : -INFINITY;
+    const float mn = fmaxf(m, wave_max(sc));   // the running max (finite: the chunk has a row)
+    const float p = valid ? expf(sc - mn) : 0.f;
+    const float f = expf(m - mn);              // (0 on the first chunk)
+    l = fmaf(l, f, wave_sum(p));
+    m = mn;
+    ps[lane] = p;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the wave's p visible to all its lanes
+
+    // p v: a lane dimensions DL lane .. DL lane + DL - 1
+#pragma unroll
+    for (int i = 0; i < DL; ++i) o[i] *= f;
+#pragma unroll 4
+    for (int t4 = 0; t4 < ATT_CHUNK / 4; ++t4) {
+      const float4 p4 = *(const float4*)(ps + 4 * t4);
+      const float pt[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const char* vrw = vs + (4 * t4 + u) * RW + DL * ES * lane;
+        if constexpr (BF && DL == 2) {
+          const uint32_t w = *(const uint32_t*)vrw;
+          o[0] = fmaf(pt[u], __uint_as_float(w << 16), o[0]);
+          o[1] = fmaf(pt[u], __uint_as_float(w & 0xFFFF0000u), o[1]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < DL; ++i) {
+            const float x = BF ? __uint_as_float((uint32_t)((const uint16_t*)vrw)[i] << 16) : ((const float*)vrw)[i];
+            o[i] = fmaf(pt[u], x, o[i]);
+          }
+        }
+      }
+    }
+    __syncthreads();  // the tiles and p are rewritten by the next chunk
   }
-  if (nchunks == 1) {  // the row's only chunk: o itself
+  if (parts == 1) {  // the row's only part: o itself
     float* ob = a.o + ((int64_t)b * a.heads + h) * HD + DL * lane;
 #pragma unroll
-    for (int i = 0; i < DL; ++i) ob[i] = o[i] / sm;
+    for (int i = 0; i < DL; ++i) ob[i] = o[i] / l;
     return;
   }
-  float* pp = a.part + (((int64_t)b * a.heads + h) * a.max_chunks + chunk) * (HD + 2);
+  float* pp = a.part + (((int64_t)b * a.heads + h) * S + split) * (HD + 2);
 #pragma unroll
   for (int i = 0; i < DL; ++i) pp[DL * lane + i] = o[i];
-  if (lane == 0) { pp[HD] = mx; pp[HD + 1] = sm; }
+  if (lane == 0) { pp[HD] = m; pp[HD + 1] = l; }
 }
 
-// The chunks of row blockIdx.y, head blockIdx.x combined, HD threads: thread t holds chunk g0 + t's statistics and
-// dimension t's values of CV chunks at a time. The first round's loads (the row's place, the statistics, the values)
-// go out together; the largest max and the sum of exp-weighted sums are workgroup reductions, each chunk's weight
-// exp(max - the largest) is computed once (by its thread) and shared through LDS. Chunks past the row's (left from
+// The parts of row blockIdx.y, head blockIdx.x combined, HD threads: thread t holds part g0 + t's statistics and
+// dimension t's values of CV parts at a time. The first round's loads (the row's place, the statistics, the values)
+// go out together; the largest max and the sum of exp-weighted sums are workgroup reductions, each part's weight
+// exp(max - the largest) is computed once (by its thread) and shared through LDS. Parts past the row's (left from
 // other calls) are selected away, never multiplied by 0.
 template <int HD>
 __device__ inline float block_fold(float v, bool is_max, float* red) {
@@ -226,15 +245,15 @@ __global__ __launch_bounds__(HD) void attention_combine(AttArgs a) {
   __shared__ float w_s[HD];
   __shared__ float red_s[HD / 64];
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const float* hp = a.part + ((int64_t)b * a.heads + h) * a.max_chunks * (HD + 2);
-  const int last = a.max_chunks - 1;
+  const float* hp = a.part + ((int64_t)b * a.heads + h) * a.splits * (HD + 2);
+  const int last = a.splits - 1;
   auto values = [&](float (&v)[CV], int c0) {
 #pragma unroll
     for (int j = 0; j < CV; ++j) v[j] = hp[(int64_t)min(c0 + j, last) * (HD + 2) + d];
   };
   float big = -INFINITY, den = 0.f, num = 0.f;
-  int nchunks = a.max_chunks;  // (the row's own count, known after the first round)
-  for (int g0 = 0; g0 < nchunks; g0 += HD) {
+  int nparts = a.splits;  // (the row's own count, known after the first round)
+  for (int g0 = 0; g0 < nparts; g0 += HD) {
     const float* pc = hp + (int64_t)min(g0 + d, last) * (HD + 2);
     const float mc = pc[HD], lc = pc[HD + 1];
     float v[CV];
@@ -242,10 +261,11 @@ __global__ __launch_bounds__(HD) void attention_combine(AttArgs a) {
     if (g0 == 0) {
       int64_t row0, length;
       row_range(a, b, row0, length);
-      nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);
-      if (nchunks == 1) return;  // the first kernel wrote o
+      const int nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);
+      nparts = nchunks < a.splits ? nchunks : a.splits;
+      if (nparts == 1) return;  // the first kernel wrote o
     }
-    const bool ok = g0 + d < nchunks;
+    const bool ok = g0 + d < nparts;
     const float top = fmaxf(big, block_fold<HD>(ok ? mc : -INFINITY, true, red_s));
     const float wc = ok ? expf(mc - top) : 0.f;
     const float f = big == -INFINITY ? 0.f : expf(big - top);
@@ -253,7 +273,7 @@ __global__ __launch_bounds__(HD) void attention_combine(AttArgs a) {
     num *= f;
     w_s[d] = wc;
     __syncthreads();
-    const int n = min(HD, nchunks - g0);
+    const int n = min(HD, nparts - g0);
     for (int j0 = 0; j0 < n; j0 += CV) {
       if (j0 > 0) values(v, g0 + j0);
 #pragma unroll
@@ -266,23 +286,29 @@ __global__ __launch_bounds__(HD) void attention_combine(AttArgs a) {
 }
 
 // the kernel, allowed its largest LDS (above 64 KiB for fp32 rows of 256 and 16 heads a key head) once
-template <int HD, int CF>
+template <int HD, int CF, bool QLDS>
 static void launch_attention(dim3 grid, dim3 block, size_t lds, hipStream_t s, const AttArgs& a) {
-  static const hipError_t allowed = hipFuncSetAttribute((const void*)attention_kernel<HD, CF>,
-      hipFuncAttributeMaxDynamicSharedMemorySize, (int)att_lds(HD, CF == FH_F32 ? 4 : 2, ATT_REP));
+  static const hipError_t allowed = hipFuncSetAttribute((const void*)attention_kernel<HD, CF, QLDS>,
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)att_lds(HD, CF == FH_F32 ? 4 : 2, ATT_REP, QLDS));
   (void)allowed;  // (a refusal shows as the launch's error)
-  hipLaunchKernelGGL((attention_kernel<HD, CF>), grid, block, lds, s, a);
+  hipLaunchKernelGGL((attention_kernel<HD, CF, QLDS>), grid, block, lds, s, a);
+}
+
+template <int HD, int CF>
+static void launch_attention(bool q_lds, dim3 grid, dim3 block, size_t lds, hipStream_t s, const AttArgs& a) {
+  if (q_lds) launch_attention<HD, CF, true>(grid, block, lds, s, a);
+  else launch_attention<HD, CF, false>(grid, block, lds, s, a);
 }
 
 template <int HD>
-static void launch_attention(int cf, dim3 grid, dim3 block, size_t lds, hipStream_t s, const AttArgs& a) {
+static void launch_attention(int cf, bool q_lds, dim3 grid, dim3 block, size_t lds, hipStream_t s, const AttArgs& a) {
   switch (cf) {
-    case FH_F32: launch_attention<HD, FH_F32>(grid, block, lds, s, a); break;
-    case FH_BF16: launch_attention<HD, FH_BF16>(grid, block, lds, s, a); break;
-    case FH_BFP8: launch_attention<HD, FH_BFP8>(grid, block, lds, s, a); break;
-    default: launch_attention<HD, FH_BFP4>(grid, block, lds, s, a); break;
+    case FH_F32: launch_attention<HD, FH_F32>(q_lds, grid, block, lds, s, a); break;
+    case FH_BF16: launch_attention<HD, FH_BF16>(q_lds, grid, block, lds, s, a); break;
+    case FH_BFP8: launch_attention<HD, FH_BFP8>(q_lds, grid, block, lds, s, a); break;
+    default: launch_attention<HD, FH_BFP4>(q_lds, grid, block, lds, s, a); break;
   }
-  if (a.max_chunks > 1) hipLaunchKernelGGL(attention_combine<HD>, dim3(a.heads, grid.z), dim3(HD), 0, s, a);
+  if (a.splits > 1) hipLaunchKernelGGL(attention_combine<HD>, dim3(a.heads, grid.z), dim3(HD), 0, s, a);
 }
 
 }  // namespace fh
@@ -329,13 +355,27 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   a.o = o;
   a.part = (float*)workspace;
   const int rep = heads / kv_heads;
-  const dim3 grid(a.max_chunks, kv_heads, batch), block(64 * rep);
-  const size_t lds = att_lds(head_dim, cache_dtype == FH_F32 ? 4 : 2, rep);
+  // S: workgroups a (row, key head), enough that the grid fills every CU as far as LDS and waves let it (all of it
+  // resident at once, each workgroup walking its chunks), at most the launch's chunks; with one chunk a workgroup, q
+  // is staged in LDS with the chunk (its scalar loads would wait behind the chunk's)
+  static int cus = 0, lds_cu = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    if (hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || lds_cu < 65536) lds_cu = 160 * 1024;
+  }
+  const int es = cache_dtype == FH_F32 ? 4 : 2;
+  const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(lds_cu / (int64_t)att_lds(head_dim, es, rep, false), 32 / rep));
+  const int64_t pairs = (int64_t)kv_heads * batch;
+  a.splits = (int)std::min<int64_t>(a.max_chunks, std::max<int64_t>(1, (cus * per_cu + pairs - 1) / pairs));
+  const bool q_lds = a.splits == a.max_chunks;
+  const size_t lds = att_lds(head_dim, es, rep, q_lds);
+  const dim3 grid(a.splits, kv_heads, batch), block(64 * rep);
   hipStream_t s = as_stream(stream);
   switch (head_dim) {
-    case 64: launch_attention<64>(cache_dtype, grid, block, lds, s, a); break;
-    case 128: launch_attention<128>(cache_dtype, grid, block, lds, s, a); break;
-    default: launch_attention<256>(cache_dtype, grid, block, lds, s, a); break;
+    case 64: launch_attention<64>(cache_dtype, q_lds, grid, block, lds, s, a); break;
+    case 128: launch_attention<128>(cache_dtype, q_lds, grid, block, lds, s, a); break;
+    default: launch_attention<256>(cache_dtype, q_lds, grid, block, lds, s, a); break;
   }
   return check_launch("fh_attention_decode");
 }

@@ -223,6 +223,27 @@ def test_attention_decode(cuda, hd, heads, kv):
   assert np.array_equal(o, o2)
 
 
+def test_attention_decode_many_rows(cuda):
+  # 16 rows x 8 key heads: few enough workgroups that each walks several chunks of its row (online softmax across
+  # them, q through scalar loads), rows shorter than the workgroups sharing them, ending inside a chunk and at its edge
+  rng = np.random.default_rng(5)
+  hd, heads, kv, part, batch = 128, 32, 8, 1000, 16
+  places = np.array([0, 1, 63, 64, 65, 127, 128, 200, 450, 511, 512, 640, 777, 900, 998, 999], np.int32)
+  first = (np.arange(batch, dtype=np.int32) * part)[::-1].copy()  # (slots in another order than the rows)
+  cache = O.bf16(rng.normal(0, 1, (2 * kv, batch * part, hd)))
+  q = rng.normal(0, 1, (batch, heads * hd)).astype(np.float32)
+  ws = ops().attention_workspace(batch, heads, hd, part)
+  o = ops().attention_decode(to_gpu(q), to_gpu(cache, torch.bfloat16), heads, kv, hd, to_gpu(places, torch.int32),
+                             to_gpu(first, torch.int32), part, ws).cpu().numpy()
+  for b in range(batch):
+    n = places[b] + 1
+    k = np.repeat(cache[:kv, first[b]:first[b] + n], heads // kv, 0)
+    v = np.repeat(cache[kv:, first[b]:first[b] + n], heads // kv, 0)
+    qq = q[b].reshape(heads, 1, hd).astype(np.float64)
+    want = (OL.softmax(qq @ k.swapaxes(-1, -2) / math.sqrt(hd)) @ v).reshape(-1)
+    assert np.abs(o[b] - want).max() <= 1e-5 * np.abs(want).max() + 1e-6, (b, places[b])
+
+
 def test_embed_and_argmax(cuda):
   rng = np.random.default_rng(7)
   table = O.bf16(rng.normal(0, 1, (100, 64)))
