@@ -97,25 +97,37 @@ class Decoder:
     self._buffers(kv, batch, context, slots)
 
   def _load(self, weights):
+    """weights: weights(name, shape) giving x @ W's layout (numpy_weights, random_weights), or a checkpoint.Checkpoint,
+    whose matrices are packed straight from its rows (fused and transposed in the packing)."""
     c, hd = self.c, self.hd
+    ck = weights if hasattr(weights, "pack") else None
     f32 = lambda t: t.to(self.device, torch.float32).contiguous()
-    gpu = lambda t: t.to(self.device)
+
+    def mat(name, K, N, fmt):
+      bw = ck.pack(name, fmt) if ck is not None else ops.pack(weights(name, (K, N)).to(self.device), fmt)
+      if (bw.K, bw.N) != (K, N): raise ValueError(f"{name}: {bw.K}x{bw.N}, the model says {K}x{N}")
+      return bw
+
+    def vec(name):
+      return ck.vector(name) if ck is not None else f32(weights(name, (1, c.dim))).reshape(-1)
+
     self.layers = []
     for l in range(c.layers):
       pre = f"layers.{l}."
       L = SimpleNamespace()
-      L.norm1 = f32(weights(pre + "input_layernorm", (1, c.dim))).reshape(-1)
-      L.norm2 = f32(weights(pre + "post_attention_layernorm", (1, c.dim))).reshape(-1)
-      L.qkv = ops.pack(gpu(weights(pre + "qkv_proj", (c.dim, self.qkv_cols))), self.prec["qkv", l])
-      L.o = ops.pack(gpu(weights(pre + "o_proj", (c.heads * hd, c.dim))), self.prec["o", l])
-      L.gate_up = ops.pack(gpu(weights(pre + "gate_up_proj", (c.dim, 2 * c.ffn))), self.prec["gate_up", l])
-      L.down = ops.pack(gpu(weights(pre + "down_proj", (c.ffn, c.dim))), self.prec["down", l])
+      L.norm1, L.norm2 = vec(pre + "input_layernorm"), vec(pre + "post_attention_layernorm")
+      L.qkv = mat(pre + "qkv_proj", c.dim, self.qkv_cols, self.prec["qkv", l])
+      L.o = mat(pre + "o_proj", c.heads * hd, c.dim, self.prec["o", l])
+      L.gate_up = mat(pre + "gate_up_proj", c.dim, 2 * c.ffn, self.prec["gate_up", l])
+      L.down = mat(pre + "down_proj", c.ffn, c.dim, self.prec["down", l])
       self.layers.append(L)
-    self.norm = f32(weights("norm", (1, c.dim))).reshape(-1)
-    embed = weights("embed", (c.vocab, c.dim))
-    self.embed = embed.to(self.device, torch.bfloat16).contiguous()  # bf16 values: a row read per token
-    head_w = embed.to(self.device).t() if c.tied else gpu(weights("embed.T", (c.dim, c.vocab)))
-    self.head = ops.pack(head_w.contiguous(), self.prec["head", None])
+    self.norm = vec("norm")
+    # the embedding in bf16 (a row read per token); the output layer its own matrix, or the embedding's rows packed
+    # as its transpose (tied)
+    self.embed = ck.table() if ck is not None else weights("embed", (c.vocab, c.dim)).to(self.device, torch.bfloat16).contiguous()
+    if ck is not None: self.head = mat("embed.T", c.dim, c.vocab, self.prec["head", None])
+    elif c.tied: self.head = ops.pack_parts([self.embed], self.prec["head", None])
+    else: self.head = mat("embed.T", c.dim, c.vocab, self.prec["head", None])
     cos, sin = rotary_tables(c, c.places)
     self.cos, self.sin = torch.from_numpy(cos).to(self.device), torch.from_numpy(sin).to(self.device)
 

@@ -50,6 +50,45 @@ def pack(w, fmt="bfp8", axis=lib.AXIS_N):
   return BfpWeight(mant, exps, K, N, fmt, axis)
 
 
+def bfp_empty(K, N, fmt="bfp8", device="cuda"):
+  """An unfilled block float W[K][N] packed along N, for pack_rows_into."""
+  mb, eb = lib.bfp_bytes(K, N, lib.DTYPES[fmt], lib.AXIS_N)
+  return BfpWeight(torch.empty(mb, dtype=torch.uint8, device=device), torch.empty(eb, dtype=torch.uint8, device=device),
+                   K, N, fmt)
+
+
+def pack_rows_into(bw, part, n0):
+  """Columns n0 .. n0 + out of bw (a W[K][N] packed along N) from part [out][K] (fp32 or bf16 on the GPU): W's columns
+  as a checkpoint stores a linear layer's rows (models/llama.py's load transposes them for x @ w, llama.py:572-604).
+  The part is packed along its first axis (FH_AXIS_K, runs of 16 down its columns), whose layout is that of its
+  transpose packed along N: run-blocks n0 / 16 .. of bw, byte for byte, with no transposed copy formed. n0 and out are
+  multiples of 16."""
+  _dev(part)
+  if bw.axis != lib.AXIS_N: raise ValueError("pack_rows_into: a weight packed along N")
+  if part.dim() != 2 or part.shape[1] != bw.K or part.dtype not in _TORCH or part.stride(1) != 1:
+    raise ValueError(f"pack_rows_into: part [out][{bw.K}] fp32 or bf16 with contiguous rows, not {tuple(part.shape)} {part.dtype}")
+  out = part.shape[0]
+  if n0 % 16 or out % 16 or n0 + out > bw.N: raise ValueError(f"pack_rows_into: columns {n0}..{n0 + out} of {bw.N} (multiples of 16)")
+  fmt = lib.DTYPES[bw.fmt]
+  m0, e0 = lib.bfp_bytes(bw.K, n0, fmt, lib.AXIS_N) if n0 else (0, 0)
+  mb, eb = lib.bfp_bytes(out, bw.K, fmt, lib.AXIS_K)
+  assert m0 + mb <= bw.mant.numel() and e0 + eb <= bw.exps.numel()
+  lib.call("fh_bfp_pack", _ptr(part), _TORCH[part.dtype], out, bw.K, part.stride(0), fmt, lib.AXIS_K,
+           ctypes.c_void_p(bw.mant.data_ptr() + m0), ctypes.c_void_p(bw.exps.data_ptr() + e0), _stream())
+
+
+def pack_parts(parts, fmt="bfp8"):
+  """W = [P0ᵀ | P1ᵀ | ...] packed along N from parts in a checkpoint's layout, P_i [out_i][K]: a fused q|k|v or
+  gate|up (models/llama.py:376-427) straight from the checkpoint's rows (pack_rows_into)."""
+  K, N = parts[0].shape[1], sum(p.shape[0] for p in parts)
+  bw = bfp_empty(K, N, fmt, parts[0].device)
+  n0 = 0
+  for p in parts:
+    pack_rows_into(bw, p, n0)
+    n0 += p.shape[0]
+  return bw
+
+
 def dequant(bw, out=None):
   """The weight's values as bf16 [K][N] (fh_bfp_dequant), bit for bit."""
   if out is None: out = torch.empty(bw.K, bw.N, dtype=torch.bfloat16, device=bw.mant.device)

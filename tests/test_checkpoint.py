@@ -1,0 +1,44 @@
+"""The checkpoint reader's host side (no GPU): config.json as models/llama.py's config reads it, tensor names as
+load keys them (Mixtral's w1/w2/w3 included), the mapped files' values, the index of two files (the reference's
+test_llama_load, test/test_sim.py:1371-1396, on this loader)."""
+import json
+import numpy as np
+import pytest
+import checkpoints as C
+from ferrite_amd import checkpoint as K
+
+
+def test_config_and_names(tmp_path):
+  rope = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
+  t = C.llama(tmp_path, np.random.default_rng(40), layers=1, rope=rope)
+  c = K.config(str(tmp_path), places=64)
+  assert (c.dim, c.heads, c.kv, c.layers, c.ffn, c.vocab, c.places, c.tied) == (256, 4, 2, 1, 384, 512, 64, False)
+  assert c.rope == rope and c.theta == 500000.0 and c.eps == 1e-5 and c.experts == 0
+  ck = K.Checkpoint(str(tmp_path))
+  assert set(ck.tensors) == {K._name(n) for n in t} and "layers.0.q_proj" in ck.tensors and "lm_head" in ck.tensors
+  for name, a in t.items():
+    got = ck.host(K._name(name))
+    assert got.dtype == a.dtype and np.array_equal(got, a), name  # (the mapped bytes as they were written)
+  assert ck._parts("layers.0.qkv_proj") == ["layers.0.q_proj", "layers.0.k_proj", "layers.0.v_proj"]
+  assert ck._parts("embed.T") == ["lm_head"]
+
+
+def test_mixtral_names_and_tied(tmp_path):
+  C.llama(tmp_path, np.random.default_rng(41), layers=1, experts=4, k=2, tied=True, two_files=False)
+  c = K.config(str(tmp_path))
+  assert (c.experts, c.k, c.tied, c.norm_topk, c.places) == (4, 2, True, True, 4096)
+  ck = K.Checkpoint(str(tmp_path))
+  assert {"layers.0.gate", "layers.0.experts.3.gate_proj", "layers.0.experts.3.down_proj", "layers.0.experts.3.up_proj"} <= set(ck.tensors)
+  assert ck._parts("embed.T") == ["embed_tokens"]  # no lm_head: the embedding's rows
+
+
+def test_refuses_what_it_cannot_read(tmp_path):
+  C.write_safetensors(tmp_path / "model.safetensors", {"model.embed_tokens.weight": np.zeros((4, 16), np.float32)})
+  header, data = K._safetensors(str(tmp_path / "model.safetensors"))
+  assert header["model.embed_tokens.weight"]["dtype"] == "F32" and data.size == 4 * 16 * 4
+  cfg = {"hidden_size": 16, "num_attention_heads": 1, "num_key_value_heads": 1, "num_hidden_layers": 1, "rms_norm_eps": 1e-5,
+         "rope_theta": 1e4, "max_position_embeddings": 32, "vocab_size": 4, "intermediate_size": 16,
+         "rope_scaling": {"rope_type": "yarn", "factor": 4.0}}
+  (tmp_path / "config.json").write_text(json.dumps(cfg))
+  with pytest.raises(NotImplementedError, match="yarn"):
+    K.config(str(tmp_path))
