@@ -306,6 +306,13 @@ class Decoder:
     self.places.add_(1)
     self.rows.add_(1)
 
+  def heads(self, k=64, inv_temp=None):
+    """The last step's logit heads (models/serve.py:31-47): each row's k best logits and their tokens, and given each
+    row's 1/temperature, the log of the sum of exp(x t) over its row (ops.logit_heads: fh_logit_heads)."""
+    if inv_temp is not None and not isinstance(inv_temp, torch.Tensor):
+      inv_temp = torch.as_tensor(inv_temp, dtype=torch.float32, device=self.device).reshape(-1)
+    return ops.logit_heads(self.logits, k, inv_temp)
+
 
 def numpy_weights(w):
   """weights(name, shape) over a dict of numpy arrays (bf16 values as float32), for Decoder."""

@@ -279,6 +279,23 @@ def moe_experts(x, ex, dense, out=None, residual=None, ssq_out=None, norm_w=None
   return out
 
 
+def logit_heads(logits, k=64, inv_temp=None, ws=None):
+  """Each row's head (fh_logit_heads; models/serve.py:31-47): its k largest logits, largest first and the first column
+  of equals first, their columns, and given inv_temp (each row's 1/temperature, [rows] fp32) the log of the sum of
+  exp(x t) over the row: (values [rows][k], ids [rows][k] int32[, lse [rows]])."""
+  _dev(logits, inv_temp)
+  if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1: raise ValueError("logit_heads: fp32 rows")
+  rows, vocab = logits.shape
+  values = torch.empty(rows, k, dtype=torch.float32, device=logits.device)
+  ids = torch.empty(rows, k, dtype=torch.int32, device=logits.device)
+  lse = torch.empty(rows, dtype=torch.float32, device=logits.device) if inv_temp is not None else None
+  n = lib.load().fh_heads_workspace_bytes(rows, vocab, k)
+  if n and (ws is None or ws.numel() < n): ws = torch.empty(n, dtype=torch.uint8, device=logits.device)
+  lib.call("fh_logit_heads", _ptr(logits), logits.stride(0), rows, vocab, k, _ptr(inv_temp), _ptr(values), _ptr(ids),
+           _ptr(lse), _ptr(ws) if n else None, ws.numel() if n else 0, _stream())
+  return (values, ids) if lse is None else (values, ids, lse)
+
+
 def argmax_rows(x, ids=None):
   _dev(x)
   if ids is None: ids = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)

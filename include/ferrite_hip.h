@@ -255,6 +255,19 @@ int fh_argmax_rows(const float* x, int64_t rows, int64_t n, int32_t* ids, void* 
 /* The same pick from the (value, column) pairs an FH_EP_STORE epilogue left in argmax_parts: parts [rows][nparts]. */
 int fh_argmax_parts(const void* parts, int64_t rows, int64_t nparts, int32_t* ids, void* stream);
 
+/* ---- logit heads (models/serve.py:31-47; Head.of, 23-27) ------------------------------------------------------
+ * Each row of logits [rows][ldl] (fp32, rows 16-byte aligned, ldl a multiple of 4): its k (1..64) largest values,
+ * largest first, the first column of equal values first (numpy's stable argsort of -x; Tensor.topk's topk_kernel,
+ * ferrite/compiler.py:1716-1838), into values [rows][k] and their columns into ids [rows][k]; and, given inv_temp
+ * (each row's 1/temperature, [rows]), lse [rows] = log of the sum over the row of exp(x t), as max t + log sum
+ * exp((x - max) t) in fp32. Selection is exact (no rounding of the values compared). A row is cut into parts of 4096
+ * columns, a workgroup each, whose k best (and sums) a second kernel merges; at most 4096 / k parts (a vocabulary of
+ * 262144 at k = 64). NaNs are not ordered as numpy orders them. Workspace: fh_heads_workspace_bytes (0 for one part),
+ * no state kept between calls. */
+size_t fh_heads_workspace_bytes(int rows, int64_t vocab, int k);
+int fh_logit_heads(const float* logits, int64_t ldl, int rows, int64_t vocab, int k, const float* inv_temp,
+                   float* values, int32_t* ids, float* lse, void* workspace, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

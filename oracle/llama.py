@@ -9,8 +9,10 @@ GPU holds (bf16, or a block float's exact values), caches are np.zeros (float64)
 the first attention and float64 after it; products are exact (mm = a @ b, llama.py:33). Each function cites the
 line it follows. The model is a plain Llama (RMSNorm, RoPE, grouped-query attention, SwiGLU) with Llama 3's RoPE
 scaling, and Mixtral's mixture of experts in the MLP's place; the reference's other families (Qwen3.5's DeltaNet,
-gpt-oss's sinks, ...) are not on this path. tests/golden holds vectors that the reference's own models/llama.py wrote
-for these functions, which tests/test_oracle_llama.py checks this restatement against.
+gpt-oss's sinks, ...) are not on this path. The reference commits no golden vectors and its models/llama.py cannot be
+imported here (Python 3.12 syntax on 3.10), so tests/test_oracle_llama.py pins this restatement against an independent
+implementation of the same models (transformers' Llama and Mixtral blocks in float64) and the invariants the
+reference's tests assert (cached decode = full recompute, chunked prefill = the whole prompt).
 """
 import math
 from types import SimpleNamespace

@@ -145,3 +145,19 @@ def test_pack_layout_roundtrip():
       lo = np.where(lo > 7, lo - 16, lo); hi = np.where(hi > 7, hi - 16, hi)
       back = np.stack([lo, hi], -1).reshape(6, 64, 16).transpose(1, 0, 2).reshape(64, 96)
     assert np.array_equal(back, q)
+
+
+def test_head_of_pinned():
+  # the heads' oracle (serve.py:23-27) against a brute-force sort by (-value, column) on rows full of ties, and its
+  # log-sum-exp against scipy's, at several temperatures
+  from scipy.special import logsumexp
+  from oracle.serve import head_of
+  rng = np.random.default_rng(50)
+  for n, k in ((7, 7), (100, 1), (300, 64), (2000, 33)):
+    x = (np.round(rng.normal(0, 2, n) * 2) / 2).astype(np.float32)  # steps of 0.5: many equal values
+    x[rng.integers(0, n, 3)] = -np.inf
+    for t in (1.0, 0.5, 2.0):
+      v, i, lse = head_of(x, t, k)
+      want = sorted(range(n), key=lambda c: (-x[c], c))[:k]
+      assert list(i) == want and np.array_equal(v, x[want])
+      assert abs(lse - logsumexp(np.float64(x) * t)) <= 1e-12 * abs(lse) + 1e-12
