@@ -92,6 +92,9 @@ struct SkinnyMoe {
 
 // x @ W for up to 64 rows a pass on the matrix cores (fh_skinny.hip); a's epilogue already checked
 int skinny_matmul(const MatArgs& a, const SkinnyMoe& moe, int fmt, int experts, hipStream_t s);
+// x @ W in 128 x 128 tiles on the matrix cores (fh_gemm.hip), gathered per expert when moe.counts is set (STORE or
+// SILU_GATE epilogues, no prologue); a's epilogue already checked
+int gemm_tiles(const MatArgs& a, const SkinnyMoe& moe, int fmt, int experts, hipStream_t s);
 
 // Checks an fh_epilogue against the matmul's shape and fills a's prologue and epilogue fields (x, weight and y
 // fields are the caller's). `who` names the entry point in messages.

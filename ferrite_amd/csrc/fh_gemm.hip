@@ -13,6 +13,11 @@
 //
 // Tiles go to the XCDs in contiguous ranges (the hardware deals workgroups round-robin over the 8 XCDs) and within a
 // range in groups of 8 row tiles, so that an XCD's L2 keeps both the weight columns and the x rows it re-reads.
+//
+// Gathered (a mixture of experts' many tokens, models/llama.py:314-329's group path): grid.y is the expert, whose
+// weight lies expert_mant / expert_exps bytes on; its rows are the first counts[e] (at most M) of its list, x row
+// x_rows[e M + r] (row e M + r where x_rows is null), output row e M + r, scaled by row_w[e M + r] (scale_rows); a
+// row tile past the expert's count returns at once, so the grid is sized for the most rows an expert can have.
 #include "fh_epilogue.h"
 
 namespace fh {
@@ -47,16 +52,33 @@ __device__ inline int64_t tile_run(const MatArgs& a, int tn, int lr) {
 }
 
 template <bool FOUR, bool XBF16, bool NORM>
-__global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tiles_m, int tiles_n) {
+__global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tiles_m, int tiles_n, SkinnyMoe g) {
   __shared__ __attribute__((aligned(16))) char smem[GM_LDS];
   __shared__ float rs_s[GM_BM];
   // stage s: x at smem + s * GM_STAGE ([128 rows][72] bf16), W after it ([128 columns][72] bf16, K-contiguous)
   float* Cs = (float*)smem;                            // [128][132]: the output tile (after the K loop)
 
-  // tile order
-  const int T = tiles_m * tiles_n;
+  // the rows of this matmul, its first output row, its weight (gathered: expert blockIdx.y's; `a` itself is left as
+  // it is: a kernel argument changed in place is copied to scratch memory)
+  int64_t M = a.M, ybase = 0;
+  const uint8_t* wmant = a.mant;
+  const uint8_t* wexps = a.exps;
   int id = blockIdx.x;
-  if (T % 8 == 0) id = (id % 8) * (T / 8) + id / 8;
+  if (g.counts) {  // the tiles of the expert's own rows, dealt to the XCDs in 8 contiguous ranges; the rest return
+    const int e = blockIdx.y;
+    M = min((int64_t)g.counts[e], a.M);
+    ybase = (int64_t)e * a.M;
+    wmant += e * g.expert_mant;
+    wexps += e * g.expert_exps;
+    tiles_m = (int)((M + GM_BM - 1) / GM_BM);
+    const int q = (tiles_m * tiles_n + 7) / 8;
+    if (id >= 8 * q) return;
+    id = (id % 8) * q + id / 8;
+    if (id >= tiles_m * tiles_n) return;
+  } else if ((tiles_m * tiles_n) % 8 == 0) {
+    id = (id % 8) * (tiles_m * tiles_n / 8) + id / 8;
+  }
+  // tile order: within a range, groups of GM_GROUP row tiles, row tile fastest
   const int per_group = GM_GROUP * tiles_n;
   const int first_m = id / per_group * GM_GROUP;
   const int gm = min(tiles_m - first_m, GM_GROUP);
@@ -69,13 +91,14 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
   // this thread's loads: x row ar (of 128), k half ah (32 values); weight run lr (of 8), rows 4 rq .. 4 rq + 3,
   // columns 8 ch .. 8 ch + 7
   const int ar = t >> 1, ah = t & 1;
-  const int64_t xrow = min(m0 + ar, a.M - 1);
-  const bool xok = m0 + ar < a.M;
+  const int64_t xr0 = min(m0 + ar, M - 1);
+  const int64_t xrow = g.counts ? (g.x_rows ? (int64_t)g.x_rows[ybase + xr0] : ybase + xr0) : xr0;
+  const bool xok = m0 + ar < M;
   const int lr = t >> 5, rq = (t & 31) >> 1, ch = t & 1;
   const int64_t nb = tile_run(a, tn, lr);
   constexpr int RB = FOUR ? 8 : 16;
-  const uint8_t* mrun = a.mant + (nb < 0 ? 0 : nb) * a.K * RB + ch * (RB / 2);
-  const uint8_t* erun = a.exps + (nb < 0 ? 0 : nb) * a.K;
+  const uint8_t* mrun = wmant + (nb < 0 ? 0 : nb) * a.K * RB + ch * (RB / 2);
+  const uint8_t* erun = wexps + (nb < 0 ? 0 : nb) * a.K;
 
   // a K step's loads, in registers: two sets, so that each step's loads have two steps' compute to arrive
   using Half = typename std::conditional<FOUR, uint32_t, uint2>::type;  // 8 of a row's 16 magnitudes
@@ -233,8 +256,8 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
     const int64_t col = run * 16 + j;
     for (int r = t >> 7; r < GM_BM; r += 2) {
       const int64_t m = m0 + r;
-      const bool ok = m < a.M && run >= 0;
-      const int64_t at = m * a.ldy + col;
+      const bool ok = m < M && run >= 0;
+      const int64_t at = (ybase + m) * a.ldy + col;
       float v = Cs[r * GM_LDC + c] * rs_s[r];
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
       if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, m, col);
@@ -263,10 +286,11 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
     const int64_t c0 = run * 16 + j;
     for (int r = t >> 6; r < GM_BM; r += 4) {
       const int64_t m = m0 + r;
-      if (m >= a.M || run < 0) continue;
+      if (m >= M || run < 0) continue;
       float x0 = Cs[r * GM_LDC + c] * rs_s[r], x1 = Cs[r * GM_LDC + c + 64] * rs_s[r];
       if (kind == FH_EP_SILU_GATE) {
-        store_out(a.y, a.y_bf16, m * a.ldy + c0, silu(x0) * x1);
+        const float sc = g.scale_rows ? g.row_w[ybase + m] : 1.f;
+        store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + c0, silu(x0) * x1 * sc);
       } else {  // FH_EP_ROPE_KV
         const int hd = a.head_dim;
         const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
@@ -287,6 +311,30 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
       }
     }
   }
+}
+
+// The tiled kernel over a's M rows (per expert, gathered, when g.counts is set: grid.y = experts)
+int gemm_tiles(const MatArgs& a, const SkinnyMoe& g, int fmt, int experts, hipStream_t s) {
+  const int64_t tiles_m = (a.M + GM_BM - 1) / GM_BM;
+  const int64_t tiles_n = a.P == 1 ? (a.N / 16 + 7) / 8 : ((int64_t)a.items + 3) / 4;
+  if (tiles_m * tiles_n >= (1LL << 31)) return fail(FH_EUNSUP, "fh_gemm_bfp: too many tiles");
+  if (g.counts && (a.ssq_in || a.kind == FH_EP_ROPE_KV || a.kind == FH_EP_RESIDUAL)) return fail(FH_EUNSUP, "gathered GEMM: STORE or SILU_GATE, no prologue");
+  // (gathered: a grid for the most rows an expert can have, in whole multiples of the 8 XCDs)
+  const int64_t tiles = g.counts ? (tiles_m * tiles_n + 7) / 8 * 8 : tiles_m * tiles_n;
+  const dim3 grid((unsigned)tiles, g.counts ? experts : 1), b(GM_THREADS);
+  const int tm = (int)tiles_m, tn = (int)tiles_n;
+  const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
+  switch (which) {
+    case 0: hipLaunchKernelGGL((gemm_kernel<false, false, false>), grid, b, 0, s, a, tm, tn, g); break;
+    case 1: hipLaunchKernelGGL((gemm_kernel<false, false, true>), grid, b, 0, s, a, tm, tn, g); break;
+    case 2: hipLaunchKernelGGL((gemm_kernel<false, true, false>), grid, b, 0, s, a, tm, tn, g); break;
+    case 3: hipLaunchKernelGGL((gemm_kernel<false, true, true>), grid, b, 0, s, a, tm, tn, g); break;
+    case 4: hipLaunchKernelGGL((gemm_kernel<true, false, false>), grid, b, 0, s, a, tm, tn, g); break;
+    case 5: hipLaunchKernelGGL((gemm_kernel<true, false, true>), grid, b, 0, s, a, tm, tn, g); break;
+    case 6: hipLaunchKernelGGL((gemm_kernel<true, true, false>), grid, b, 0, s, a, tm, tn, g); break;
+    default: hipLaunchKernelGGL((gemm_kernel<true, true, true>), grid, b, 0, s, a, tm, tn, g); break;
+  }
+  return FH_OK;
 }
 
 }  // namespace fh
@@ -313,21 +361,7 @@ extern "C" int fh_gemm_bfp(const void* x, int x_dtype, int64_t ldx, int64_t M, i
     const SkinnyMoe none = {};
     return skinny_matmul(a, none, fmt, 1, s);
   }
-  const int64_t tiles_m = (M + GM_BM - 1) / GM_BM;
-  const int64_t tiles_n = a.P == 1 ? (N / 16 + 7) / 8 : ((int64_t)a.items + 3) / 4;
-  if (tiles_m * tiles_n >= (1LL << 31)) return fail(FH_EUNSUP, "fh_gemm_bfp: too many tiles");
-  const dim3 g((unsigned)(tiles_m * tiles_n)), b(GM_THREADS);
-  const int tm = (int)tiles_m, tn = (int)tiles_n;
-  const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
-  switch (which) {
-    case 0: hipLaunchKernelGGL((gemm_kernel<false, false, false>), g, b, 0, s, a, tm, tn); break;
-    case 1: hipLaunchKernelGGL((gemm_kernel<false, false, true>), g, b, 0, s, a, tm, tn); break;
-    case 2: hipLaunchKernelGGL((gemm_kernel<false, true, false>), g, b, 0, s, a, tm, tn); break;
-    case 3: hipLaunchKernelGGL((gemm_kernel<false, true, true>), g, b, 0, s, a, tm, tn); break;
-    case 4: hipLaunchKernelGGL((gemm_kernel<true, false, false>), g, b, 0, s, a, tm, tn); break;
-    case 5: hipLaunchKernelGGL((gemm_kernel<true, false, true>), g, b, 0, s, a, tm, tn); break;
-    case 6: hipLaunchKernelGGL((gemm_kernel<true, true, false>), g, b, 0, s, a, tm, tn); break;
-    default: hipLaunchKernelGGL((gemm_kernel<true, true, true>), g, b, 0, s, a, tm, tn); break;
-  }
+  const SkinnyMoe none = {};
+  if (int rc = gemm_tiles(a, none, fmt, 1, s)) return rc;
   return check_launch("fh_gemm_bfp");
 }

@@ -137,16 +137,31 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(const float* x, int64_t l
                                                        int E, uint16_t* xn, int32_t* counts, int32_t* rows_of,
                                                        float* row_w, int32_t* slot) {
   __shared__ float red_s[4];
+  __shared__ int wave_n[4];
   const int r = blockIdx.x, t = threadIdx.x;
-  if (r == n) {
-    for (int e = t; e < E; e += 256) {
-      int c = 0;
-      for (int i = 0; i < n; ++i) {
-        const float w = dense[(int64_t)i * E + e];
-        if (w != 0.f) { rows_of[e * n + c] = i; row_w[e * n + c] = w; slot[i * E + e] = c; ++c; }
-        else slot[i * E + e] = -1;
+  if (r == n) {  // each expert's rows in order: a thread a row, its place among the expert's by a workgroup count
+    const int lane = t & 63, wave = t >> 6;
+    for (int e = 0; e < E; ++e) {
+      int base = 0;
+      for (int i0 = 0; i0 < n; i0 += 256) {
+        const int i = i0 + t;
+        const float w = i < n ? dense[(int64_t)i * E + e] : 0.f;
+        const uint64_t picked = __ballot(w != 0.f);
+        const int before = __builtin_amdgcn_mbcnt_hi((uint32_t)(picked >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)picked, 0u));
+        if (lane == 0) wave_n[wave] = __popcll(picked);
+        __syncthreads();
+        int off = base, total = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) { off += v < wave ? wave_n[v] : 0; total += wave_n[v]; }
+        if (i < n) {
+          const int c = off + before;
+          if (w != 0.f) { rows_of[e * n + c] = i; row_w[e * n + c] = w; slot[i * E + e] = c; }
+          else slot[i * E + e] = -1;
+        }
+        base += total;
+        __syncthreads();  // (wave_n is rewritten next)
       }
-      counts[e] = c;
+      if (t == 0) counts[e] = base;
     }
     return;
   }
@@ -227,8 +242,16 @@ extern "C" int fh_moe_route(const float* x, int64_t ldx, int rows, int64_t dim, 
   return check_launch("fh_moe_route");
 }
 
+// Rows a pass: up to 64 rows (a decode step's), one pass through the skinny kernel, each touched expert's weight read
+// once; past 64 (a prompt's), passes of up to 1024 through the tiled GEMM, an expert's weight read once for every 128
+// of its rows (models/llama.py:314-329: the touched path for a decode step, the group path past it; the reference
+// turns at 128 tokens, here the tiled GEMM is already faster from 65: 560 us against 680 for two skinny passes at the
+// Mixtral shape). A pass's workspace holds each expert's whole pass of rows (a `dense` may pick every expert for a
+// row): ~370 MB for 1024 rows at the Mixtral shape; passes of 2048 were 13% faster at 2048 tokens for twice that.
+static int64_t moe_pass(int64_t rows) { return rows > 64 ? 1024 : 64; }
+
 extern "C" size_t fh_moe_workspace_bytes(int rows, int experts, int64_t ffn, int64_t dim) {
-  const int64_t r = rows < 64 ? rows : 64;  // a pass of up to 64 rows
+  const int64_t r = rows < moe_pass(rows) ? rows : moe_pass(rows);  // a pass's rows
   if (r < 1 || experts < 1 || ffn < 1 || dim < 1) return 0;
   return moe_space(r, experts, ffn, dim).total;
 }
@@ -251,8 +274,9 @@ extern "C" int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim
   if (int rc = fh_bfp_bytes(dim, gu_n, gu_fmt, FH_AXIS_N, &mb, &eb)) return rc;
   size_t dmb, deb;
   if (int rc = fh_bfp_bytes(ffn, dim, down_fmt, FH_AXIS_N, &dmb, &deb)) return rc;
-  for (int r0 = 0; r0 < rows; r0 += 64) {  // 64 rows a pass
-    const int n = rows - r0 < 64 ? rows - r0 : 64;
+  const int pass = (int)moe_pass(rows);
+  for (int r0 = 0; r0 < rows; r0 += pass) {
+    const int n = rows - r0 < pass ? rows - r0 : pass;
     const MoeSpace m = moe_space(n, experts, ffn, dim);
     char* w = (char*)workspace;
     int32_t* counts = (int32_t*)(w + m.counts);
@@ -277,7 +301,7 @@ extern "C" int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim
     SkinnyMoe moe = {};
     moe.expert_mant = (int64_t)mb; moe.expert_exps = (int64_t)eb; moe.experts = experts; moe.scale_rows = 1;
     moe.counts = counts; moe.x_rows = rows_of; moe.row_w = row_w;
-    if (int rc = skinny_matmul(a, moe, gu_fmt, experts, s)) return rc;
+    if (int rc = n > 64 ? gemm_tiles(a, moe, gu_fmt, experts, s) : skinny_matmul(a, moe, gu_fmt, experts, s)) return rc;
     // down, each expert on its own rows of g
     MatArgs d = {};
     fh_epilogue de = {};
@@ -290,7 +314,7 @@ extern "C" int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim
     SkinnyMoe dm = {};
     dm.expert_mant = (int64_t)dmb; dm.expert_exps = (int64_t)deb; dm.experts = experts; dm.scale_rows = 0;
     dm.counts = counts;
-    if (int rc = skinny_matmul(d, dm, down_fmt, experts, s)) return rc;
+    if (int rc = n > 64 ? gemm_tiles(d, dm, down_fmt, experts, s) : skinny_matmul(d, dm, down_fmt, experts, s)) return rc;
     hipLaunchKernelGGL(moe_sum_kernel, dim3(n, (unsigned)((dim + 255) / 256)), dim3(256), 0, s, parts, slot, experts, n,
                        (int)dim, residual ? residual + (int64_t)r0 * dim : nullptr, y + (int64_t)r0 * dim,
                        ssq_out ? ssq_out + (int64_t)r0 * (dim / 16) : nullptr);
