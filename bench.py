@@ -191,9 +191,10 @@ def moe_rate(T=32, reps=20):
   ms = timed_graph(run, reps, stream)
   touched = int((state["dense"] != 0).any(0).sum())
   nbytes = touched * (ex.gate_up.nbytes + ex.down.nbytes) // E + dim * E * 2 + T * dim * 4 * 2
+  flops = 2 * T * k * dim * 3 * ffn  # (each token's k experts: gate_up 2 ffn and down ffn columns of dim)
   return {"workload": f"config 5: Mixtral-shape MoE layer, {T} tokens, {E} experts bfp4, top {k}", "us": round(ms * 1e3, 2),
           "experts_touched": touched, "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
-          "frac": round(nbytes / ms * 1e3 / HBM_PEAK, 4)}
+          "frac": round(nbytes / ms * 1e3 / HBM_PEAK, 4), "tflops": round(flops / ms / 1e9, 1)}
 
 
 def measured_traffic(kernel, config, batch):
@@ -324,6 +325,9 @@ def main():
     extra["moe"] = moe_rate()
     print(f"# {extra['moe']['workload']}: {extra['moe']['us']:.1f} us, {extra['moe']['gbs']:.0f} GB/s "
           f"({extra['moe']['frac']:.1%}), {extra['moe']['experts_touched']} experts touched", file=sys.stderr, flush=True)
+    extra["moe_prompt"] = moe_rate(2048, reps=5)  # (a prompt's tokens: the group path, on the matrix cores)
+    print(f"# {extra['moe_prompt']['workload']}: {extra['moe_prompt']['us']:.1f} us, {extra['moe_prompt']['tflops']:.0f} TFLOP/s "
+          f"({extra['moe_prompt']['tflops'] * 1e12 / MFMA_PEAK:.1%} of {MFMA_PEAK / 1e15:.1f} PFLOP/s)", file=sys.stderr, flush=True)
   pre = None
   if not args.no_prefill and args.config == "c3":
     pre = prefill_rate()
