@@ -96,7 +96,7 @@ class Tensor:
     tensor._bf16s's). Waits for the launches queued."""
     x = self.realize()
     if x.dtype in BFP:
-      t = x.rt.run(lambda: ops.dequant(x.data))[None]
+      t = x.rt.run(lambda: torch.stack([ops.dequant(w) for w in _matrices(x)]))
     else:
       if not x.data.is_contiguous(): x = (x + 0).realize()  # a view: copied by our kernel first
       t = x.data
@@ -179,16 +179,16 @@ class Tensor:
   def cast(self, dtype):
     """To another dtype; to a block float, packed at once (fh_bfp_pack, Tensor.cast's bfp4_kernel / packer)."""
     if dtype == self.dtype: return self
-    if dtype in BFP:
+    if dtype in BFP:  # (a batch: each matrix packed, a mixture's experts for matmul(index=))
       x = self.realize()
-      assert x.batch == 1, "a block float of one matrix"
       if x.dtype == "int32" or not x.data.is_contiguous(): x = (x.float() if x.dtype == "int32" else x + 0).realize()
-      out = Tensor(self.rt, self.rows, self.cols, batch=1, dtype=dtype)
-      out.data = x.rt.run(lambda: ops.pack(x.data[0], dtype))
+      out = Tensor(self.rt, self.rows, self.cols, batch=x.batch, dtype=dtype)
+      packed = [x.rt.run(lambda b=b: ops.pack(x.data[b], dtype)) for b in range(x.batch)]
+      out.data = packed[0] if x.batch == 1 else packed
       return out
     if self.dtype in BFP:  # a block float's values (each a bf16 value)
-      b = Tensor(self.rt, self.rows, self.cols, batch=1, dtype="bf16")
-      b.data = self.rt.run(lambda: ops.dequant(self.data))[None]
+      b = Tensor(self.rt, self.rows, self.cols, batch=self.batch, dtype="bf16")
+      b.data = self.rt.run(lambda: torch.stack([ops.dequant(w) for w in _matrices(self)]))
       return b.cast(dtype)
     return Tensor(self.rt, self.rows, self.cols, "cast", (self,), self.batch, dtype)
 
@@ -258,22 +258,65 @@ class Tensor:
     c = self - self.mean(axis)
     return c * ((c * c).mean(axis) + eps).rsqrt()
 
+  def topk(self, k, parts=1, labels=None):
+    """Each row's k (<= 64) largest values, largest first, and their columns (int32), the first column of equal values
+    first (Tensor.topk, ferrite/tensor.py:373-388: numpy's stable order), by fh_logit_heads. ferrite's parts and labels
+    split a row too wide for a worker's L1 into two topk calls; one call here takes a whole row (parts 1, no labels)."""
+    if parts != 1 or labels is not None: raise NotImplementedError("topk: one call selects over a whole row (parts=1, labels=None)")
+    assert self.dtype in ("bf16", "fp32") and 1 <= k <= min(self.cols, 64), "bf16 or fp32, k of at most 64"
+    n, cols = self.batch * self.rows, self.cols
+    ld = (cols + 3) // 4 * 4  # rows 16-byte aligned for the kernel's loads
+    x = torch.empty(n, ld, dtype=torch.float32, device=self.rt.device)
+    prog, inputs = _fit_program(self.float() if self.dtype != "fp32" else self, self.shape, allow_acc=False)
+    p = _cprogram(prog, inputs)
+    self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(x), lib.F32, *self.shape, self.rows * ld, ld, ops._stream()))
+    values, ids = self.rt.run(lambda: ops.logit_heads(x[:, :cols], k))
+    v = Tensor(self.rt, self.rows, k, batch=self.batch, dtype="fp32")
+    v.data = values.reshape(self.batch, self.rows, k)
+    i = Tensor(self.rt, self.rows, k, batch=self.batch, dtype="int32")
+    i.data = ids.reshape(self.batch, self.rows, k)
+    return (v if self.dtype == "fp32" else v.cast(self.dtype)), i
+
   # ---- matmul (ferrite/tensor.py:443-485) ----------------------------------------------------------------------------
   def __matmul__(self, x): return self.matmul(x)
 
-  def matmul(self, x, dtype=None):
+  def matmul(self, x, dtype=None, fidelity=None, index=None):
     """self (1 x rows x K) @ x (K x N, a block float: bfp8 or bfp4, cast once), written as dtype: bf16, or fp32 if
     self is, unless said. fp32 rows, a few, go through the exact-product GEMV; otherwise the matrix cores take self's
     values in bf16, as ferrite's chip does (bf16 rows: exact products too); the elementwise ops on top of it run in
-    the same kernel."""
+    the same kernel. fidelity: the chip's product phases (ferrite/tensor.py:443-452); taken and ignored, the products
+    here being exact or bf16 x bf16 whatever it says. index: an int32 (rows, k) tensor choosing, for each batch entry b
+    of the result, which of x's matrices (x a batch of block floats: a mixture's experts) multiplies self's entry b (or
+    its only one), index's (b // k, b % k); an entry choosing none (x.batch or more) is zeros. It is resolved on the GPU
+    (each matrix's product, then each entry's pick), so a recording replays it; ops.moe_experts is the path that reads
+    only the chosen experts."""
     if x.dtype not in BFP: raise NotImplementedError("matmul: B is a block float (bfp8 or bfp4) on this runtime")
+    if index is not None:
+      assert index.dtype == "int32" and self.cols == x.rows and self.batch in (1, index.rows * index.cols) and index.batch == 1, \
+        f"{self.shape} @ {x.shape} picked by {index.shape} {index.dtype}"
+      return Tensor(self.rt, self.rows, x.cols, "picked", (self, x.realize(), index), index.rows * index.cols,
+                    dtype or ("fp32" if self.dtype == "fp32" else "bf16"))
+    assert x.batch == 1, "a batch of block floats is read through index="
     assert self.batch == 1 and self.cols == x.rows and self.dtype != "int32", f"{self.shape} @ {x.shape}"
     return Tensor(self.rt, self.rows, x.cols, "matmul", (self, x.realize()), 1, dtype or ("fp32" if self.dtype == "fp32" else "bf16"))
 
   # ---- realizing ----------------------------------------------------------------------------------------------------
-  def realize(self):
-    """Compute it now (if it is an op), into memory of its own; returns it, realized."""
+  def realize(self, into=None):
+    """Compute it now (if it is an op), into memory of its own, or into `into`'s (a stored tensor of the same shape and
+    dtype, rows contiguous: jit's copies of its inputs); returns it, realized."""
+    if into is not None:
+      assert into.data is not None and into.shape == self.shape and into.dtype == self.dtype and into.dtype not in BFP
+      assert into.data.is_contiguous(), "realize(into=): a tensor of its own memory"
+      if self is into: return into
+      prog, inputs = _fit_program(self, self.shape, allow_acc=False)  # (a stored tensor: one copy op)
+      p = _cprogram(prog, inputs)
+      out, ld = into.data, into.data.stride()
+      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[into.dtype], *into.shape, ld[0], ld[1], ops._stream()))
+      return into
     if self.data is not None: return self
+    if self.op == "picked":
+      self._done(_picked(self).data)
+      return self
     if self.op in REDUCE:
       f, axis = REDUCE[self.op]
       src = self.srcs[0]
@@ -313,6 +356,76 @@ class Tensor:
     self.data, self.op, self.srcs, self.args = data, None, (), ()
 
 
+def _matrices(t):
+  """A block-float tensor's matrices (BfpWeights)."""
+  return t.data if isinstance(t.data, list) else [t.data]
+
+
+def _picked(t):
+  """matmul(index=): each of x's matrices times self's rows (all entries' rows at once), then each entry keeps the
+  product of the matrix its index names (keep/drop: selected, never multiplied by 0)."""
+  a, w, index = t.srcs
+  mats = _matrices(w)
+  n = t.batch
+  rows = a.realize()
+  flat = rows.reshape(1, rows.batch * rows.rows, rows.cols)  # every entry's rows, one matrix
+  choice = index.realize().reshape(n, 1, 1)
+  acc = None
+  for e, m in enumerate(mats):
+    we = Tensor(t.rt, w.rows, w.cols, batch=1, dtype=w.dtype)
+    we.data = m
+    y = flat.matmul(we, t.dtype).realize().reshape(rows.batch, rows.rows, w.cols)
+    pick = choice.eq(e)
+    acc = (pick.where(y, 0.0) if acc is None else pick.where(y, acc)).realize()
+  return acc
+
+
+class Recording:
+  """A function's launches captured once as a HIP graph on its runtime's stream (ferrite's Recording, tensor.py:775-785:
+  launches recorded once and sent again as one block); send() replays them."""
+
+  def __init__(self, rt): self.rt, self.graph = rt, torch.cuda.CUDAGraph()
+
+  def __enter__(self):
+    self._ctx = torch.cuda.graph(self.graph, stream=self.rt.stream)
+    self._ctx.__enter__()
+    return self
+
+  def __exit__(self, *exc): return self._ctx.__exit__(*exc)
+
+  def send(self):
+    with torch.cuda.stream(self.rt.stream):
+      self.graph.replay()
+
+
+def jit(f):
+  """f, a function of tensors that returns one, run from a recording (ferrite's jit, tensor.py:788-810): its first call
+  runs as any would (so every kernel and table is set up), its second is captured as a HIP graph (each launch, and the
+  memory it writes, kept from then on) and replayed, and each later call copies its inputs into the second call's
+  (a launch each) and replays the graph: one host call for the whole step. Its inputs keep their shapes and dtypes;
+  nothing else it reads may change, and it may not read back. Its result is the same tensor every call, written again by
+  the next."""
+  calls, inputs, out, rec = 0, (), None, None
+
+  def run(*xs):
+    nonlocal calls, inputs, out, rec
+    calls, rt = calls + 1, xs[0].rt
+    if calls == 1: return f(*xs).realize()
+    if calls == 2:
+      inputs = [x.realize() if x.data is not None and x.data.is_contiguous() else (x + 0).realize() for x in xs]
+      rt.wait()
+      with Recording(rt) as rec:
+        out = f(*inputs).realize()
+      rec.send()
+      return out
+    for x, to in zip(xs, inputs):
+      assert (x.shape, x.dtype) == (to.shape, to.dtype), f"{x.shape} {x.dtype} where the recording had {to.shape} {to.dtype}"
+      if x is not to: x.realize(into=to)
+    rec.send()
+    return out
+  return run
+
+
 def _walk(t, seen=None):
   """The unrealized nodes under t (t first), each once."""
   seen = set() if seen is None else seen
@@ -326,7 +439,7 @@ def _ops(t, acc_ok):
   """How many program ops t's tree would take, counting each shared node once and stopping at what realizes apart."""
   n = 0
   for u in _walk(t):
-    if u.op in REDUCE or (u.op == "matmul" and not acc_ok): continue
+    if u.op in REDUCE or u.op == "picked" or (u.op == "matmul" and not acc_ok): continue
     if u.op == "matmul": n += 1; continue
     n += 1
   return n
@@ -340,8 +453,8 @@ def _fit_program(root, shape, allow_acc):
     readers = {}
     for u in _walk(root):
       for s in u.srcs: readers[id(s)] = readers.get(id(s), 0) + 1
-    for u in list(_walk(root)):  # reductions (a reduction's own operand too) and every matmul but the root's chain's
-      if u.op in REDUCE: u.realize()  # first are realized apart
+    for u in list(_walk(root)):  # reductions (a reduction's own operand too), picked matmuls, and every matmul but
+      if u.op in REDUCE or u.op == "picked": u.realize()  # the root's chain's first are realized apart
     accs = [u for u in _walk(root) if u.op == "matmul"]
     for i, u in enumerate(accs):
       if not allow_acc or i > 0 or readers.get(id(u), 0) > 1 or u.shape != tuple(shape): u.realize()

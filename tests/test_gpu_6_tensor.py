@@ -176,3 +176,66 @@ def test_long_tree_in_parts(rt):
     z = (z * 0.9 + 0.1).relu() if i % 2 else z * 1.01 - 0.02
     want = np.maximum(want * 0.9 + 0.1, 0) if i % 2 else want * 1.01 - 0.02
   close(z.numpy()[0], want, 1e-5, "long")
+
+
+def test_jit_replays_the_recording(rt):
+  # ferrite's jit (tensor.py:788-810): the first call runs, the second is captured as a HIP graph and replayed, later
+  # calls copy their inputs in and replay; each call's result equals the same expression run eagerly, bit for bit
+  # (the same kernels), with eager work between the replays
+  from ferrite_amd import tensor
+  rng = np.random.default_rng(66)
+  w = Tn().of(rt, rng.normal(0, 0.05, (64, 48)).tolist(), "fp32").cast("bfp8")
+  b = Tn().of(rt, rng.normal(0, 1, (1, 48)).tolist(), "fp32")
+  f = tensor.jit(lambda x: ((x @ w) + b).relu().softmax())
+  out = None
+  for i in range(5):
+    x = Tn().of(rt, rng.normal(0, 1, (3, 64)).tolist(), "fp32")
+    got = f(x)
+    if i >= 2: assert got is out, "the recording's result, every call"
+    out = got
+    got = np.array(got.tolist(), np.float32)
+    want = np.array((((x @ w) + b).relu().softmax()).tolist(), np.float32)
+    assert np.array_equal(got, want), i
+    assert np.allclose(got.sum(-1), 1, atol=1e-5)
+
+
+def test_matmul_picked_by_index(rt):
+  # matmul(index=) (tensor.py:443-460): each batch entry multiplies the block float its index names (a mixture's
+  # experts), an index past the batch gives zeros; entries of one row each, and one shared row; fidelity is taken
+  rng = np.random.default_rng(67)
+  E, K, N = 3, 64, 48
+  W = rng.normal(0, 0.05, (E, K, N)).astype(np.float32)
+  wb = Tn().of(rt, W.tolist(), "fp32").cast("bfp8")
+  assert wb.shape == (E, K, N)
+  assert np.array_equal(np.array(wb.float().tolist(), np.float32), np.stack([O.bfp(W[e]) for e in range(E)]).astype(np.float32))
+  idx = np.array([[0, 2], [1, 1], [2, 0], [3, 1]], np.int32)
+  index = Tn().of(rt, idx.tolist(), "int32")
+  X = rng.normal(0, 1, (8, 1, K)).astype(np.float32)
+  y = Tn().of(rt, X.tolist(), "fp32").matmul(wb, "fp32", fidelity=2, index=index)
+  assert y.shape == (8, 1, N)
+  got = np.array(y.tolist(), np.float64)
+  for b in range(8):
+    e = idx[b // 2, b % 2]
+    want = X[b] @ O.bfp(W[e]) if e < E else np.zeros((1, N))
+    assert np.abs(got[b] - want).max() <= 2e-6 * (np.abs(X[b]) @ np.abs(W[min(e, E - 1)])).max() + 1e-6, b
+  one = rng.normal(0, 1, (1, K)).astype(np.float32)
+  y1 = np.array(Tn().of(rt, one.tolist(), "fp32").matmul(wb, "fp32", index=index).tolist(), np.float64)
+  for b in range(8):
+    e = idx[b // 2, b % 2]
+    want = one @ O.bfp(W[e]) if e < E else np.zeros((1, N))
+    assert np.abs(y1[b] - want).max() <= 1e-5 * np.abs(want).max() + 1e-6, b
+
+
+def test_topk(rt):
+  # Tensor.topk (tensor.py:373-388): largest first, the first column of equals first, bf16 and fp32, a batch of rows,
+  # a width that is not a multiple of 4
+  rng = np.random.default_rng(68)
+  a = np.round(rng.normal(0, 2, (2, 5, 301)) * 2) / 2
+  for dtype in ("bf16", "fp32"):
+    t = Tn().of(rt, a.tolist(), dtype)
+    v, i = t.topk(20)
+    assert v.dtype == dtype and i.dtype == "int32" and v.shape == i.shape == (2, 5, 20)
+    ids = np.array(i.tolist())
+    want = np.argsort(-a, -1, kind="stable")[..., :20]
+    assert np.array_equal(ids, want), dtype
+    assert np.array_equal(np.array(v.tolist()), np.take_along_axis(a, want, -1))
