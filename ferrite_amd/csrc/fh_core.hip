@@ -164,25 +164,37 @@ extern "C" int fh_bfp_dequant(const void* mant, const uint8_t* exps, int64_t K, 
   return check_launch("fh_bfp_dequant");
 }
 
-// ---- embedding rows: one workgroup a row --------------------------------------------------------------------------
+// ---- embedding rows: one workgroup a row, a thread a run of 16 columns ----------------------------------------------
+// (each thread's run loaded at once, written, and its sum of squares taken from the registers: no barrier, no re-read)
 template <bool BF16>
 __global__ __launch_bounds__(256) void embed_kernel(const void* __restrict__ table, int64_t vocab, int64_t dim,
                                                     const int32_t* __restrict__ ids, float* __restrict__ x,
                                                     float* __restrict__ ssq) {
-  int b = blockIdx.x;
+  const int b = blockIdx.x;
   int64_t id = ids[b];
   if (id < 0 || id >= vocab) id = 0;  // (the host checks ids it knows; one computed on the GPU reads row 0 rather than fault)
-  for (int64_t c = threadIdx.x; c < dim; c += blockDim.x) {
-    float v = BF16 ? bf16_to_f(((const uint16_t*)table)[id * dim + c]) : ((const float*)table)[id * dim + c];
-    x[b * dim + c] = v;
-  }
-  __syncthreads();
-  if (ssq) {
-    for (int64_t p = threadIdx.x; p < dim / 16; p += blockDim.x) {
-      float s = 0;
-      for (int j = 0; j < 16; ++j) { float v = x[b * dim + p * 16 + j]; s = fmaf(v, v, s); }
-      ssq[b * (dim / 16) + p] = s;
+  for (int64_t run = threadIdx.x; run < dim / 16; run += blockDim.x) {
+    float v[16];
+    if (BF16) {
+      const uint4* src = (const uint4*)((const uint16_t*)table + id * dim + run * 16);
+      const uint4 lo = src[0], hi = src[1];
+      const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { v[2 * j] = __uint_as_float(w[j] << 16); v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u); }
+    } else {
+      const float4* src = (const float4*)((const float*)table + id * dim + run * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) { const float4 f = src[q]; v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w; }
     }
+    float4* dst = (float4*)(x + b * dim + run * 16);
+    float sq = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sq = fmaf(v[4 * q + j], v[4 * q + j], sq);
+    }
+    if (ssq) ssq[b * (dim / 16) + run] = sq;
   }
 }
 
@@ -191,6 +203,7 @@ extern "C" int fh_embed_rows(const void* table, int table_dtype, int64_t vocab, 
   if (!table || !ids || !x) return fail(FH_EINVAL, "fh_embed_rows: null pointer");
   if (vocab <= 0 || dim <= 0 || batch <= 0 || dim % 16) return fail(FH_EINVAL, "fh_embed_rows: bad sizes (dim a multiple of 16)");
   if (table_dtype != FH_F32 && table_dtype != FH_BF16) return fail(FH_EINVAL, "fh_embed_rows: table is FH_F32 or FH_BF16");
+  if (((uintptr_t)table & 15) || ((uintptr_t)x & 15)) return fail(FH_EINVAL, "fh_embed_rows: table and x 16-byte aligned (runs of 16 loaded whole)");
   hipStream_t s = as_stream(stream);
   if (table_dtype == FH_BF16) hipLaunchKernelGGL((embed_kernel<true>), dim3(batch), dim3(256), 0, s, table, vocab, dim, ids, x, ssq_out);
   else hipLaunchKernelGGL((embed_kernel<false>), dim3(batch), dim3(256), 0, s, table, vocab, dim, ids, x, ssq_out);
@@ -231,27 +244,37 @@ extern "C" int fh_argmax_rows(const float* x, int64_t rows, int64_t n, int32_t* 
 }
 
 // ---- argmax from the GEMV's per-run pairs: one workgroup a row ---------------------------------------------------
-__global__ __launch_bounds__(256) void argmax_parts_kernel(const int2* __restrict__ parts, int64_t n, int32_t* __restrict__ ids) {
+// (1024 threads, each issuing its 8 loads of a round before comparing any: one memory round trip a round)
+constexpr int AP_T = 1024, AP_U = 8;
+__global__ __launch_bounds__(AP_T) void argmax_parts_kernel(const int2* __restrict__ parts, int64_t n, int32_t* __restrict__ ids) {
   const int2* row = parts + (int64_t)blockIdx.x * n;
   float best = -INFINITY;
   int at = INT32_MAX;
-  for (int64_t c = threadIdx.x; c < n; c += blockDim.x) {
-    const int2 p = row[c];
-    const float v = __int_as_float(p.x);
-    if (v > best || (v == best && p.y < at)) { best = v; at = p.y; }
+  for (int64_t c0 = 0; c0 < n; c0 += AP_T * AP_U) {
+    int2 p[AP_U];
+#pragma unroll
+    for (int u = 0; u < AP_U; ++u) {
+      const int64_t c = c0 + (int64_t)u * AP_T + threadIdx.x;
+      p[u] = c < n ? row[c] : make_int2(__float_as_int(-INFINITY), INT32_MAX);
+    }
+#pragma unroll
+    for (int u = 0; u < AP_U; ++u) {
+      const float v = __int_as_float(p[u].x);
+      if (v > best || (v == best && p[u].y < at)) { best = v; at = p[u].y; }
+    }
   }
   for (int m = 32; m >= 1; m >>= 1) {
     const float ov = __shfl_xor(best, m, 64);
     const int oa = __shfl_xor(at, m, 64);
     if (ov > best || (ov == best && oa < at)) { best = ov; at = oa; }
   }
-  __shared__ float bv[4];
-  __shared__ int ba[4];
+  __shared__ float bv[AP_T / 64];
+  __shared__ int ba[AP_T / 64];
   const int w = threadIdx.x / 64;
   if ((threadIdx.x & 63) == 0) { bv[w] = best; ba[w] = at; }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int i = 1; i < 4; ++i)
+    for (int i = 1; i < AP_T / 64; ++i)
       if (bv[i] > best || (bv[i] == best && ba[i] < at)) { best = bv[i]; at = ba[i]; }
     ids[blockIdx.x] = at == INT32_MAX ? 0 : at;
   }
@@ -259,6 +282,6 @@ __global__ __launch_bounds__(256) void argmax_parts_kernel(const int2* __restric
 
 extern "C" int fh_argmax_parts(const void* parts, int64_t rows, int64_t nparts, int32_t* ids, void* stream) {
   if (!parts || !ids || rows <= 0 || nparts <= 0) return fail(FH_EINVAL, "fh_argmax_parts: bad arguments");
-  hipLaunchKernelGGL(argmax_parts_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), (const int2*)parts, nparts, ids);
+  hipLaunchKernelGGL(argmax_parts_kernel, dim3((unsigned)rows), dim3(AP_T), 0, as_stream(stream), (const int2*)parts, nparts, ids);
   return check_launch("fh_argmax_parts");
 }

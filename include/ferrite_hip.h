@@ -167,7 +167,7 @@ int fh_gemm_bfp(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, i
 /* ---- the rest of a decode step ------------------------------------------------------------------------------- */
 
 /* Rows ids[batch] of an embedding table [vocab][dim] (fp32 or bf16) into x[batch][dim] fp32, with the sums of
- * squares by 16 columns into ssq_out[batch][dim/16] (for the first block's RMSNorm). Replaces the gather of
+ * squares by 16 columns into ssq_out[batch][dim/16] (for the first block's RMSNorm). table and x 16-byte aligned. Replaces the gather of
  * forward's first line (models/llama.py:472; Tensor.gather, ferrite/tensor.py:116-126). */
 int fh_embed_rows(const void* table, int table_dtype, int64_t vocab, int64_t dim, const int32_t* ids, int batch,
                   float* x, float* ssq_out, void* stream);
