@@ -22,60 +22,127 @@ namespace fh {
 
 constexpr int RT_THREADS = 256;
 
-template <bool RBF16>
+// REG (dim a multiple of 16, at most 4096, x rows 16-byte aligned): a thread holds dimensions 16 t .. 16 t + 15 of the
+// row in registers, each loaded once, and issues all its router rows of a group of 8 experts together; otherwise the
+// row goes through LDS a dimension a thread at a time (a second pass of registers took every VGPR: the compiler hoists
+// its loads over the first pass's arithmetic)
+constexpr int RT_RUN = 16, RT_PASS = RT_THREADS * RT_RUN, RT_MAXP = 1;
+
+template <bool RBF16, bool REG>
 __global__ __launch_bounds__(RT_THREADS) void route_kernel(const float* x, int64_t ldx, int dim, const float* norm_w,
                                                            float eps, int centered, const void* router, int E, int k,
                                                            int norm_topk, int32_t* ids, float* wts, float* dense) {
-  extern __shared__ float rt_smem[];   // [dim] the normed row
+  extern __shared__ float rt_smem[];   // [dim] the normed row (the generic path)
   __shared__ float logit_s[256];
   __shared__ float red_s[RT_THREADS / 64];
   const int64_t row = blockIdx.x;
   const float* xr = x + row * ldx;
   const int t = threadIdx.x;
   float* h = rt_smem;
+  float hr[RT_MAXP][RT_RUN];  // (REG) this thread's dimensions, normed
   // the row, normed
-  float rs = 1.f;
-  if (norm_w) {
+  if constexpr (REG) {
     float s = 0.f;
-    for (int i = t; i < dim; i += RT_THREADS) s += xr[i] * xr[i];
-    s = wave_sum(s);
-    if ((t & 63) == 0) red_s[t >> 6] = s;
+#pragma unroll
+    for (int p = 0; p < RT_MAXP; ++p) {
+      const int c = p * RT_PASS + RT_RUN * t;
+#pragma unroll
+      for (int q = 0; q < RT_RUN / 4; ++q) {
+        const float4 f = c < dim ? *(const float4*)(xr + c + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+        hr[p][4 * q] = f.x; hr[p][4 * q + 1] = f.y; hr[p][4 * q + 2] = f.z; hr[p][4 * q + 3] = f.w;
+      }
+#pragma unroll
+      for (int j = 0; j < RT_RUN; ++j) s = fmaf(hr[p][j], hr[p][j], s);
+    }
+    if (norm_w) {
+      s = wave_sum(s);
+      if ((t & 63) == 0) red_s[t >> 6] = s;
+      __syncthreads();
+      float tot = 0.f;
+      for (int w = 0; w < RT_THREADS / 64; ++w) tot += red_s[w];
+      const float rs = 1.0f / sqrtf(tot / (float)dim + eps);
+#pragma unroll
+      for (int p = 0; p < RT_MAXP; ++p) {
+        const int c = p * RT_PASS + RT_RUN * t;
+        if (c >= dim) continue;
+#pragma unroll
+        for (int q = 0; q < RT_RUN / 4; ++q) {
+          float4 g = *(const float4*)(norm_w + c + 4 * q);
+          if (centered) { g.x += 1.f; g.y += 1.f; g.z += 1.f; g.w += 1.f; }
+          hr[p][4 * q] *= rs * g.x; hr[p][4 * q + 1] *= rs * g.y; hr[p][4 * q + 2] *= rs * g.z; hr[p][4 * q + 3] *= rs * g.w;
+        }
+      }
+    }
+  } else {
+    float rs = 1.f;
+    if (norm_w) {
+      float s = 0.f;
+      for (int i = t; i < dim; i += RT_THREADS) s += xr[i] * xr[i];
+      s = wave_sum(s);
+      if ((t & 63) == 0) red_s[t >> 6] = s;
+      __syncthreads();
+      float tot = 0.f;
+      for (int w = 0; w < RT_THREADS / 64; ++w) tot += red_s[w];
+      rs = 1.0f / sqrtf(tot / (float)dim + eps);
+    }
+    for (int i = t; i < dim; i += RT_THREADS) {
+      const float g = norm_w ? (centered ? norm_w[i] + 1.f : norm_w[i]) : 1.f;
+      h[i] = norm_w ? xr[i] * rs * g : xr[i];
+    }
     __syncthreads();
-    float tot = 0.f;
-    for (int w = 0; w < RT_THREADS / 64; ++w) tot += red_s[w];
-    rs = 1.0f / sqrtf(tot / (float)dim + eps);
   }
-  for (int i = t; i < dim; i += RT_THREADS) {
-    const float g = norm_w ? (centered ? norm_w[i] + 1.f : norm_w[i]) : 1.f;
-    h[i] = norm_w ? xr[i] * rs * g : xr[i];
-  }
-  __syncthreads();
-  // logits, 8 experts at a time: thread t takes the router's rows t, t + 256, .. (a row's 8 values one 16-byte load
-  // where the layout allows), then the workgroup sums each expert's partials in a fixed order
+  // logits, 8 experts at a time (a router row's 8 values one 16-byte load where the layout allows), then the
+  // workgroup sums each expert's partials in a fixed order
   constexpr int EC = 8;
   __shared__ float part8[RT_THREADS / 64][EC];
   const bool wide = RBF16 && E % 8 == 0;
+  auto weight = [&](int64_t d, int e) {
+    return RBF16 ? bf16_to_f(((const uint16_t*)router)[d * E + e]) : ((const float*)router)[d * E + e];
+  };
   for (int e0 = 0; e0 < E; e0 += EC) {
     float acc[EC];
 #pragma unroll
     for (int j = 0; j < EC; ++j) acc[j] = 0.f;
-#pragma unroll 4
-    for (int i = t; i < dim; i += RT_THREADS) {
-      const float hv = h[i];
-      if (wide) {
-        const uint4 w = *(const uint4*)((const uint16_t*)router + (int64_t)i * E + e0);
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    if constexpr (REG) {
+      auto pass = [&](const float (&hv)[RT_RUN], int c) {  // a pass's 16 router rows in flight at once
+        if (c >= dim) return;
+        if (wide) {
+          uint4 w[RT_RUN];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[2 * j] = fmaf(hv, __uint_as_float(ww[j] << 16), acc[2 * j]);
-          acc[2 * j + 1] = fmaf(hv, __uint_as_float(ww[j] & 0xFFFF0000u), acc[2 * j + 1]);
+          for (int i = 0; i < RT_RUN; ++i) w[i] = *(const uint4*)((const uint16_t*)router + (int64_t)(c + i) * E + e0);
+#pragma unroll
+          for (int i = 0; i < RT_RUN; ++i) {
+            const uint32_t ww[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              acc[2 * j] = fmaf(hv[i], __uint_as_float(ww[j] << 16), acc[2 * j]);
+              acc[2 * j + 1] = fmaf(hv[i], __uint_as_float(ww[j] & 0xFFFF0000u), acc[2 * j + 1]);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < RT_RUN; ++i)
+#pragma unroll
+            for (int j = 0; j < EC; ++j) acc[j] = fmaf(hv[i], weight(c + i, min(e0 + j, E - 1)), acc[j]);
         }
-      } else {
+      };
+      static_assert(RT_MAXP == 1, "one pass");
+      pass(hr[0], RT_RUN * t);
+    } else {
+#pragma unroll 4
+      for (int i = t; i < dim; i += RT_THREADS) {
+        const float hv = h[i];
+        if (wide) {
+          const uint4 w = *(const uint4*)((const uint16_t*)router + (int64_t)i * E + e0);
+          const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int j = 0; j < EC; ++j) {
-          const int e = min(e0 + j, E - 1);
-          const float w = RBF16 ? bf16_to_f(((const uint16_t*)router)[(int64_t)i * E + e]) : ((const float*)router)[(int64_t)i * E + e];
-          acc[j] = fmaf(hv, w, acc[j]);
+          for (int j = 0; j < 4; ++j) {
+            acc[2 * j] = fmaf(hv, __uint_as_float(ww[j] << 16), acc[2 * j]);
+            acc[2 * j + 1] = fmaf(hv, __uint_as_float(ww[j] & 0xFFFF0000u), acc[2 * j + 1]);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < EC; ++j) acc[j] = fmaf(hv, weight(i, min(e0 + j, E - 1)), acc[j]);
         }
       }
     }
@@ -232,13 +299,18 @@ extern "C" int fh_moe_route(const float* x, int64_t ldx, int rows, int64_t dim, 
   if (rows < 1 || dim < 1 || ldx < dim) return fail(FH_EINVAL, "fh_moe_route: need rows, dim >= 1, ldx >= dim");
   if (experts < 1 || experts > 256 || k < 1 || k > 16 || k > experts) return fail(FH_EUNSUP, "fh_moe_route: 1 <= k <= 16, k <= experts <= 256");
   if (router_dtype != FH_F32 && router_dtype != FH_BF16) return fail(FH_EINVAL, "fh_moe_route: router is FH_F32 or FH_BF16");
-  const size_t lds = (size_t)dim * sizeof(float);
+  // (the register path for a decode step's rows, where each workgroup's latency is the time; many rows keep the lean
+  // kernel, more of whose workgroups fit a CU)
+  const bool reg = rows <= 512 && dim % RT_RUN == 0 && dim <= RT_MAXP * RT_PASS && ldx % 4 == 0 && !((uintptr_t)x & 15) &&
+                   !((uintptr_t)norm_w & 15) && !((uintptr_t)router & 15);
+  const size_t lds = reg ? 0 : (size_t)dim * sizeof(float);
   if (lds > 120 * 1024) return fail(FH_EUNSUP, "fh_moe_route: row too long");
   hipStream_t s = as_stream(stream);
-  if (router_dtype == FH_BF16)
-    hipLaunchKernelGGL((route_kernel<true>), dim3(rows), dim3(RT_THREADS), lds, s, x, ldx, (int)dim, norm_w, eps, centered, router, experts, k, norm_topk, ids, weights, dense);
-  else
-    hipLaunchKernelGGL((route_kernel<false>), dim3(rows), dim3(RT_THREADS), lds, s, x, ldx, (int)dim, norm_w, eps, centered, router, experts, k, norm_topk, ids, weights, dense);
+  const dim3 g(rows), b(RT_THREADS);
+  if (router_dtype == FH_BF16 && reg) hipLaunchKernelGGL((route_kernel<true, true>), g, b, lds, s, x, ldx, (int)dim, norm_w, eps, centered, router, experts, k, norm_topk, ids, weights, dense);
+  else if (router_dtype == FH_BF16) hipLaunchKernelGGL((route_kernel<true, false>), g, b, lds, s, x, ldx, (int)dim, norm_w, eps, centered, router, experts, k, norm_topk, ids, weights, dense);
+  else if (reg) hipLaunchKernelGGL((route_kernel<false, true>), g, b, lds, s, x, ldx, (int)dim, norm_w, eps, centered, router, experts, k, norm_topk, ids, weights, dense);
+  else hipLaunchKernelGGL((route_kernel<false, false>), g, b, lds, s, x, ldx, (int)dim, norm_w, eps, centered, router, experts, k, norm_topk, ids, weights, dense);
   return check_launch("fh_moe_route");
 }
 
