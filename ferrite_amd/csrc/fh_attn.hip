@@ -222,6 +222,195 @@ __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(AttArgs a) {
   if (lane == 0) { pp[HD] = m; pp[HD + 1] = l; }
 }
 
+// The same chunk walk on the matrix cores, for a workgroup that takes several chunks (the throughput case: many rows)
+// of a bf16 or block-float cache: 4 waves, wave w the chunk's rows 16 w .. 16 w + 15 for every query head at once
+// (v_mfma_f32_16x16x32_bf16, heads as N). Scores S = K q^T: A the keys' rows from the LDS tile, B q in three bf16
+// terms that sum to it exactly (each the next 8 significant bits), so the products stay fp32-exact. The softmax
+// statistics of each head meet across the waves in LDS; p is written to LDS in three bf16 terms; O += p V with A
+// p's terms and B the values' columns read transposed (ds_read_b64_tr_b16), wave w a quarter of the dimensions.
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 att_bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float att_floatx4;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short att_short4;
+#define ATT_LDS __attribute__((address_space(3)))
+constexpr int ATT_PS = ATT_CHUNK + 8;  // a head's row of p in LDS, bf16 (144 bytes)
+
+// x as three floats with bf16 values whose sum is x exactly (truncations to 8 significant bits, then the rest's)
+__device__ inline void split3(float x, float& t1, float& t2, float& t3) {
+  t1 = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
+  const float r1 = x - t1;
+  t2 = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
+  t3 = r1 - t2;
+}
+__device__ inline uint32_t pack_hi(float lo, float hi) {  // two floats with bf16 values: their high halves
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+static size_t att_mfma_lds(int hd) {
+  return (size_t)2 * ATT_CHUNK * att_row_bytes(hd, 2) + (size_t)3 * 16 * ATT_PS * 2 + (size_t)(2 * 4 * 16 + 3 * 16) * 4;
+}
+
+template <int HD, int CF>
+__global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
+  using Loader = ChunkLoader<HD, CF>;
+  constexpr int RW = Loader::RW, RWS = RW / 2;   // a tile row in bytes and in bf16s
+  constexpr int KS = HD / 32;                    // K steps of the scores
+  constexpr int TPW = HD / 16 / 4;               // 16-column tiles of O a wave
+  static_assert(CF != FH_F32 && TPW >= 1, "bf16 or block-float tiles, head_dim >= 64");
+  extern __shared__ __attribute__((aligned(16))) char att_smem[];
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, S = a.splits;
+  const int rep = a.heads / a.kv_heads;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), g = lane >> 4, c16 = lane & 15;
+  int64_t row0, length;
+  row_range(a, b, row0, length);
+  const int nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);
+  if (split >= nchunks) return;
+  const int parts = nchunks < S ? nchunks : S;
+  char* ks = att_smem;
+  char* vs = att_smem + ATT_CHUNK * RW;
+  uint16_t* ps = (uint16_t*)(att_smem + 2 * ATT_CHUNK * RW);          // [3][16 heads][ATT_PS]
+  float* wmax_s = (float*)(ps + 3 * 16 * ATT_PS);                     // [4 waves][16 heads]
+  float* wsum_s = wmax_s + 64;
+  float* m_s = wsum_s + 64;                                           // [16] running max
+  float* l_s = m_s + 16;                                              // [16] running sum
+  float* f_s = l_s + 16;                                              // [16] this chunk's rescale
+  if (tid < 16) { m_s[tid] = -INFINITY; l_s[tid] = 0.f; f_s[tid] = 0.f; }
+  const int64_t krow0 = (int64_t)kvh * a.cache_len + row0, vrow0 = (int64_t)(a.kv_heads + kvh) * a.cache_len + row0;
+  auto rows_of = [&](int c) { return (int)(length - (int64_t)c * ATT_CHUNK < ATT_CHUNK ? length - (int64_t)c * ATT_CHUNK : ATT_CHUNK); };
+
+  Loader ld;
+  ld.load(a, krow0 + (int64_t)split * ATT_CHUNK, vrow0 + (int64_t)split * ATT_CHUNK, rows_of(split), 0, tid, 256);
+
+  // q as B: lane's head c16 (zero past rep), dimensions 32 s + 8 g .. + 7, three terms
+  att_bf16x8 qb[KS][3];
+  {
+    const bool hv = c16 < rep;
+    const float* qh = a.q + ((int64_t)b * a.heads + (int64_t)kvh * rep + (hv ? c16 : 0)) * HD + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const float4 u = *(const float4*)(qh + 32 * s), v = *(const float4*)(qh + 32 * s + 4);
+      const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+      float t[3][8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) split3(hv ? x[i] : 0.f, t[0][i], t[1][i], t[2][i]);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const uint4 pk = make_uint4(pack_hi(t[j][0], t[j][1]), pack_hi(t[j][2], t[j][3]), pack_hi(t[j][4], t[j][5]), pack_hi(t[j][6], t[j][7]));
+        qb[s][j] = *(const att_bf16x8*)&pk;
+      }
+    }
+  }
+  att_floatx4 acc_o[TPW];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) acc_o[tt] = att_floatx4{0.f, 0.f, 0.f, 0.f};
+  // the values' transposed reads: 16-lane group g reads rows 8 g .. of a 32-row step; lane 4 m + q of a group points
+  // at row m, columns 4 q .. 4 q + 3 of a 16-column tile
+  ATT_LDS att_short4* vtr = (ATT_LDS att_short4*)((uint16_t*)vs + (8 * g + ((lane & 15) >> 2)) * RWS + 4 * (lane & 3));
+
+  for (int c = split; c < nchunks; c += S) {
+    const int n = rows_of(c);
+    const int64_t kr = krow0 + (int64_t)c * ATT_CHUNK, vr = vrow0 + (int64_t)c * ATT_CHUNK;
+    ld.store(ks, vs, 0, tid, 256);
+    for (int i0 = 4 * 256; i0 < Loader::PIECES; i0 += 4 * 256) {
+      ld.load(a, kr, vr, n, i0, tid, 256);
+      ld.store(ks, vs, i0, tid, 256);
+    }
+    __syncthreads();
+    if (c + S < nchunks)  // the next chunk's first round in flight during this one's arithmetic
+      ld.load(a, kr + (int64_t)S * ATT_CHUNK, vr + (int64_t)S * ATT_CHUNK, rows_of(c + S), 0, tid, 256);
+
+    // scores: rows 16 w + 4 g + i (i < 4) of head c16 in lane's D
+    att_floatx4 sc = att_floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const att_bf16x8 ka = *(const att_bf16x8*)(ks + (16 * w + c16) * RW + (32 * s + 8 * g) * 2);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[s][j], sc, 0, 0, 0);
+    }
+    const bool hv = c16 < rep;
+    float sv[4], wm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = hv && 16 * w + 4 * g + i < n;
+      sv[i] = ok ? sc[i] * a.scale : -INFINITY;
+      wm = fmaxf(wm, sv[i]);
+    }
+    wm = fmaxf(wm, __shfl_xor(wm, 16, 64));
+    wm = fmaxf(wm, __shfl_xor(wm, 32, 64));
+    if (g == 0) wmax_s[w * 16 + c16] = wm;
+    __syncthreads();
+    float mn = m_s[c16];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) mn = fmaxf(mn, wmax_s[v * 16 + c16]);
+    float pv[4], wsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { pv[i] = sv[i] == -INFINITY ? 0.f : expf(sv[i] - mn); wsum += pv[i]; }
+    wsum += __shfl_xor(wsum, 16, 64);
+    wsum += __shfl_xor(wsum, 32, 64);
+    if (g == 0) wsum_s[w * 16 + c16] = wsum;
+    {  // p's three terms: head c16, rows 16 w + 4 g .. + 3
+      float t[3][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) split3(pv[i], t[0][i], t[1][i], t[2][i]);
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        *(uint2*)(ps + (j * 16 + c16) * ATT_PS + 16 * w + 4 * g) = make_uint2(pack_hi(t[j][0], t[j][1]), pack_hi(t[j][2], t[j][3]));
+    }
+    __syncthreads();
+    if (tid < 16) {  // each head's running statistics
+      float mh = m_s[tid], sum = 0.f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) { mh = fmaxf(mh, wmax_s[v * 16 + tid]); sum += wsum_s[v * 16 + tid]; }
+      const float f = tid < rep && mh != -INFINITY ? expf(m_s[tid] - mh) : 0.f;  // (0 on the first chunk)
+      l_s[tid] = fmaf(l_s[tid], f, sum);
+      m_s[tid] = mh;
+      f_s[tid] = f;
+    }
+    __syncthreads();
+    // O (heads 4 g + i, dimensions of tile w TPW + tt) rescaled, then += p V over the chunk's two 32-row steps
+    float fr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fr[i] = f_s[4 * g + i];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc_o[tt][i] *= fr[i];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      att_bf16x8 pa[3];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) pa[j] = *(const att_bf16x8*)(ps + (j * 16 + c16) * ATT_PS + 32 * s2 + 8 * g);
+#pragma unroll
+      for (int tt = 0; tt < TPW; ++tt) {
+        const int col = 16 * (w * TPW + tt);
+        const att_short4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vtr + (32 * s2 * RWS + col) / 4);
+        const att_short4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vtr + (32 * s2 * RWS + 4 * RWS + col) / 4);
+        const short v8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const att_bf16x8 vb = *(const att_bf16x8*)v8;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc_o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[j], vb, acc_o[tt], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // the tiles, p and the statistics are rewritten by the next chunk
+  }
+  // lane's outputs: heads 4 g + i, dimension 16 (w TPW + tt) + c16
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hh = 4 * g + i;
+    if (hh >= rep) continue;
+    const int64_t h = (int64_t)kvh * rep + hh;
+    if (parts == 1) {
+      float* ob = a.o + ((int64_t)b * a.heads + h) * HD;
+#pragma unroll
+      for (int tt = 0; tt < TPW; ++tt) ob[16 * (w * TPW + tt) + c16] = acc_o[tt][i] / l_s[hh];
+    } else {
+      float* pp = a.part + (((int64_t)b * a.heads + h) * S + split) * (HD + 2);
+#pragma unroll
+      for (int tt = 0; tt < TPW; ++tt) pp[16 * (w * TPW + tt) + c16] = acc_o[tt][i];
+      if (w == 0 && c16 == 0) { pp[HD] = m_s[hh]; pp[HD + 1] = l_s[hh]; }
+    }
+  }
+}
+
 // The parts of row blockIdx.y, head blockIdx.x combined, HD threads: thread t holds part g0 + t's statistics and
 // dimension t's values of CV parts at a time. The first round's loads (the row's place, the statistics, the values)
 // go out together; the largest max and the sum of exp-weighted sums are workgroup reductions, each part's weight
@@ -311,6 +500,24 @@ static void launch_attention(int cf, bool q_lds, dim3 grid, dim3 block, size_t l
   if (a.splits > 1) hipLaunchKernelGGL(attention_combine<HD>, dim3(a.heads, grid.z), dim3(HD), 0, s, a);
 }
 
+template <int HD, int CF>
+static void launch_attention_mfma(dim3 grid, dim3 block, hipStream_t s, const AttArgs& a) {
+  static const hipError_t allowed = hipFuncSetAttribute((const void*)attention_mfma<HD, CF>,
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)att_mfma_lds(HD));
+  (void)allowed;
+  hipLaunchKernelGGL((attention_mfma<HD, CF>), grid, block, att_mfma_lds(HD), s, a);
+}
+
+template <int HD>
+static void launch_attention_mfma(int cf, dim3 grid, dim3 block, hipStream_t s, const AttArgs& a) {
+  switch (cf) {
+    case FH_BF16: launch_attention_mfma<HD, FH_BF16>(grid, block, s, a); break;
+    case FH_BFP8: launch_attention_mfma<HD, FH_BFP8>(grid, block, s, a); break;
+    default: launch_attention_mfma<HD, FH_BFP4>(grid, block, s, a); break;
+  }
+  if (a.splits > 1) hipLaunchKernelGGL(attention_combine<HD>, dim3(a.heads, grid.z), dim3(HD), 0, s, a);
+}
+
 }  // namespace fh
 
 using namespace fh;
@@ -365,13 +572,27 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
     if (hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || lds_cu < 65536) lds_cu = 160 * 1024;
   }
   const int es = cache_dtype == FH_F32 ? 4 : 2;
-  const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(lds_cu / (int64_t)att_lds(head_dim, es, rep, false), 32 / rep));
   const int64_t pairs = (int64_t)kv_heads * batch;
-  a.splits = (int)std::min<int64_t>(a.max_chunks, std::max<int64_t>(1, (cus * per_cu + pairs - 1) / pairs));
+  auto splits_for = [&](int64_t lds_bytes, int64_t waves) {
+    const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(lds_cu / lds_bytes, 32 / waves));
+    return (int)std::min<int64_t>(a.max_chunks, std::max<int64_t>(1, (cus * per_cu + pairs - 1) / pairs));
+  };
+  hipStream_t s = as_stream(stream);
+  // the matrix cores where workgroups walk several chunks (many rows: throughput) of a bf16 or block-float cache
+  if (cache_dtype != FH_F32 && head_dim <= 128) {
+    const int sm = splits_for((int64_t)att_mfma_lds(head_dim), 4);
+    if (sm < a.max_chunks) {
+      a.splits = sm;
+      const dim3 grid(a.splits, kv_heads, batch), block(256);
+      if (head_dim == 64) launch_attention_mfma<64>(cache_dtype, grid, block, s, a);
+      else launch_attention_mfma<128>(cache_dtype, grid, block, s, a);
+      return check_launch("fh_attention_decode");
+    }
+  }
+  a.splits = splits_for((int64_t)att_lds(head_dim, es, rep, false), rep);
   const bool q_lds = a.splits == a.max_chunks;
   const size_t lds = att_lds(head_dim, es, rep, q_lds);
   const dim3 grid(a.splits, kv_heads, batch), block(64 * rep);
-  hipStream_t s = as_stream(stream);
   switch (head_dim) {
     case 64: launch_attention<64>(cache_dtype, q_lds, grid, block, lds, s, a); break;
     case 128: launch_attention<128>(cache_dtype, q_lds, grid, block, lds, s, a); break;

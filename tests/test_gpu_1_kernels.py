@@ -223,25 +223,39 @@ def test_attention_decode(cuda, hd, heads, kv):
   assert np.array_equal(o, o2)
 
 
-def test_attention_decode_many_rows(cuda):
-  # 16 rows x 8 key heads: few enough workgroups that each walks several chunks of its row (online softmax across
-  # them, q through scalar loads), rows shorter than the workgroups sharing them, ending inside a chunk and at its edge
-  rng = np.random.default_rng(5)
-  hd, heads, kv, part, batch = 128, 32, 8, 1000, 16
-  places = np.array([0, 1, 63, 64, 65, 127, 128, 200, 450, 511, 512, 640, 777, 900, 998, 999], np.int32)
+@pytest.mark.parametrize("hd,heads,kv,batch,part", [(128, 32, 8, 16, 1000), (64, 9, 3, 64, 600)])
+def test_attention_decode_many_rows(cuda, hd, heads, kv, batch, part):
+  # many rows x key heads: few enough workgroups that each walks several chunks of its row (online softmax across
+  # them; a bf16 or block-float cache takes the matrix cores, q and p in three bf16 terms each), rows shorter than the
+  # workgroups sharing them, ending inside a chunk and at its edge; a block float's values read bit for bit as the
+  # same values in a bf16 cache
+  rng = np.random.default_rng(5 + hd)
+  places = rng.integers(0, part, batch).astype(np.int32)
+  places[:6] = [0, 1, 63, 64, part - 1, part - 2]
   first = (np.arange(batch, dtype=np.int32) * part)[::-1].copy()  # (slots in another order than the rows)
   cache = O.bf16(rng.normal(0, 1, (2 * kv, batch * part, hd)))
   q = rng.normal(0, 1, (batch, heads * hd)).astype(np.float32)
   ws = ops().attention_workspace(batch, heads, hd, part)
-  o = ops().attention_decode(to_gpu(q), to_gpu(cache, torch.bfloat16), heads, kv, hd, to_gpu(places, torch.int32),
-                             to_gpu(first, torch.int32), part, ws).cpu().numpy()
-  for b in range(batch):
-    n = places[b] + 1
-    k = np.repeat(cache[:kv, first[b]:first[b] + n], heads // kv, 0)
-    v = np.repeat(cache[kv:, first[b]:first[b] + n], heads // kv, 0)
-    qq = q[b].reshape(heads, 1, hd).astype(np.float64)
-    want = (OL.softmax(qq @ k.swapaxes(-1, -2) / math.sqrt(hd)) @ v).reshape(-1)
-    assert np.abs(o[b] - want).max() <= 1e-5 * np.abs(want).max() + 1e-6, (b, places[b])
+  args = (heads, kv, hd, to_gpu(places, torch.int32), to_gpu(first, torch.int32), part, ws)
+  for cd in (torch.bfloat16, torch.float32):
+    o = ops().attention_decode(to_gpu(q), to_gpu(cache, cd), *args).cpu().numpy()
+    for b in range(batch):
+      n = places[b] + 1
+      k = np.repeat(cache[:kv, first[b]:first[b] + n], heads // kv, 0)
+      v = np.repeat(cache[kv:, first[b]:first[b] + n], heads // kv, 0)
+      qq = q[b].reshape(heads, 1, hd).astype(np.float64)
+      want = (OL.softmax(qq @ k.swapaxes(-1, -2) / math.sqrt(hd)) @ v).reshape(-1)
+      assert np.abs(o[b] - want).max() <= 1e-5 * np.abs(want).max() + 1e-6, (cd, b, places[b])
+  for fmt in ("bfp8", "bfp4"):
+    same = O.bfp(cache, fmt).astype(np.float32)
+    c = ops().kv_cache(2 * kv, batch * part, hd, fmt)
+    qv, top = O.bfp_parts(cache, fmt)
+    mant = qv.astype(np.int8).view(np.uint8).reshape(-1) if fmt == "bfp8" else \
+        ((qv[..., 0::2] & 15) | ((qv[..., 1::2] & 15) << 4)).astype(np.uint8).reshape(-1)
+    c.data.copy_(torch.from_numpy(np.concatenate([mant, top.astype(np.uint8).reshape(-1)])).cuda())
+    got = ops().attention_decode(to_gpu(q), c, *args).cpu()
+    want = ops().attention_decode(to_gpu(q), to_gpu(same, torch.bfloat16), *args).cpu()
+    assert torch.equal(got, want), fmt
 
 
 def test_embed_and_argmax(cuda):
