@@ -30,9 +30,14 @@ struct AttArgs {
   const int32_t* places; const int32_t* first_row;
   int max_chunks;       // the launch's context in chunks (a row reads at most this many)
   int splits;           // S: workgroups a (row, key head), = gridDim.x
-  float* o;
+  void* o; int o_bf16;  // the output, fp32 or bf16 (rounded to nearest even)
   float* part;          // [batch][heads][splits][hd + 2]: p v, then max, then sum
 };
+
+__device__ inline void put_o(const AttArgs& a, int64_t at, float v) {
+  if (a.o_bf16) ((uint16_t*)a.o)[at] = (uint16_t)bf16_rne_f(v);
+  else ((float*)a.o)[at] = v;
+}
 
 // the row's cache rows, kept inside the cache and the launch's chunks whatever the places say
 __device__ inline void row_range(const AttArgs& a, int b, int64_t& row0, int64_t& length) {
@@ -211,9 +216,9 @@ __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(AttArgs a) {
     __syncthreads();  // the tiles and p are rewritten by the next chunk
   }
   if (parts == 1) {  // the row's only part: o itself
-    float* ob = a.o + ((int64_t)b * a.heads + h) * HD + DL * lane;
+    const int64_t ob = ((int64_t)b * a.heads + h) * HD + DL * lane;
 #pragma unroll
-    for (int i = 0; i < DL; ++i) ob[i] = o[i] / l;
+    for (int i = 0; i < DL; ++i) put_o(a, ob + i, o[i] / l);
     return;
   }
   float* pp = a.part + (((int64_t)b * a.heads + h) * S + split) * (HD + 2);
@@ -399,9 +404,9 @@ __global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
     if (hh >= rep) continue;
     const int64_t h = (int64_t)kvh * rep + hh;
     if (parts == 1) {
-      float* ob = a.o + ((int64_t)b * a.heads + h) * HD;
+      const int64_t ob = ((int64_t)b * a.heads + h) * HD;
 #pragma unroll
-      for (int tt = 0; tt < TPW; ++tt) ob[16 * (w * TPW + tt) + c16] = acc_o[tt][i] / l_s[hh];
+      for (int tt = 0; tt < TPW; ++tt) put_o(a, ob + 16 * (w * TPW + tt) + c16, acc_o[tt][i] / l_s[hh]);
     } else {
       float* pp = a.part + (((int64_t)b * a.heads + h) * S + split) * (HD + 2);
 #pragma unroll
@@ -471,7 +476,7 @@ __global__ __launch_bounds__(HD) void attention_combine(AttArgs a) {
     __syncthreads();  // (w_s is rewritten by the next group)
     big = top;
   }
-  a.o[((int64_t)b * a.heads + h) * HD + d] = num / den;
+  put_o(a, ((int64_t)b * a.heads + h) * HD + d, num / den);
 }
 
 // the kernel, allowed its largest LDS (above 64 KiB for fp32 rows of 256 and 16 heads a key head) once
@@ -541,7 +546,8 @@ extern "C" size_t fh_kv_cache_bytes(int cache_dtype, int kv_heads, int64_t cache
 
 extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch,
                                    int heads, int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row,
-                                   int64_t max_context, float* o, void* workspace, size_t ws_bytes, void* stream) {
+                                   int64_t max_context, void* o, int o_dtype, void* workspace, size_t ws_bytes,
+                                   void* stream) {
   if (!q || !cache || !places || !first_row || !o) return fail(FH_EINVAL, "fh_attention_decode: null pointer");
   if (batch < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads)
     return fail(FH_EINVAL, "fh_attention_decode: heads must be a multiple of kv_heads");
@@ -550,6 +556,7 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   if (cache_dtype < FH_F32 || cache_dtype > FH_BFP4)
     return fail(FH_EUNSUP, "fh_attention_decode: cache is FH_F32, FH_BF16, FH_BFP8 or FH_BFP4");
   if (max_context < 1 || max_context > cache_len) return fail(FH_EINVAL, "fh_attention_decode: max_context outside 1..cache_len");
+  if (o_dtype != FH_F32 && o_dtype != FH_BF16) return fail(FH_EINVAL, "fh_attention_decode: o is FH_F32 or FH_BF16");
   const size_t need = fh_attention_workspace_bytes(batch, heads, head_dim, max_context);
   if (max_context > ATT_CHUNK && (!workspace || ws_bytes < need))
     return fail(FH_EINVAL, "fh_attention_decode: workspace smaller than fh_attention_workspace_bytes");
@@ -559,7 +566,7 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   a.heads = heads; a.kv_heads = kv_heads; a.scale = 1.0f / sqrtf((float)head_dim);
   a.places = places; a.first_row = first_row;
   a.max_chunks = (int)((max_context + ATT_CHUNK - 1) / ATT_CHUNK);
-  a.o = o;
+  a.o = o; a.o_bf16 = o_dtype == FH_BF16;
   a.part = (float*)workspace;
   const int rep = heads / kv_heads;
   // S: workgroups a (row, key head), enough that the grid fills every CU as far as LDS and waves let it (all of it

@@ -152,6 +152,7 @@ class Decoder:
     self.h = z(B, c.ffn)
     self.xn = torch.zeros(B, c.dim, dtype=torch.bfloat16, device=self.device)   # the matrix cores' bf16 rows (each residual epilogue's copy)
     self.hb = torch.zeros(B, c.ffn, dtype=torch.bfloat16, device=self.device)
+    self.attb = torch.zeros(B, c.heads * hd, dtype=torch.bfloat16, device=self.device)  # attention's rows for o's matrix cores
     self.logits = z(B, c.vocab)
     self.picks = torch.zeros(B, dtype=torch.int32, device=self.device)
     self.parts = torch.zeros(B, c.vocab // 16, dtype=torch.int64, device=self.device)  # each run of 16 logits' best
@@ -222,8 +223,8 @@ class Decoder:
         ops.gemm(self.xn, L.qkv, ops.epilogue(lib.EP_ROPE_KV, **rope), out=self.q)
       else:
         ops.gemm(self.xn, L.qkv, ops.epilogue(lib.EP_ROPE_KV, **rs, **rope), out=self.q)
-      ops.attention_decode(self.q, self.cache[l], c.heads, c.kv, hd, self.places, self.first, self.context, self.ws, o=self.att)
-      ops.gemm(self.att, L.o, ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq, copy_bf16=self.xn,
+      ops.attention_decode(self.q, self.cache[l], c.heads, c.kv, hd, self.places, self.first, self.context, self.ws, o=self.attb)
+      ops.gemm(self.attb, L.o, ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq, copy_bf16=self.xn,
                                            copy_w=nw[2 * l + 1]), out=self.x)
       ops.gemm(self.xn, L.gate_up, ops.epilogue(lib.EP_SILU_GATE, split=c.ffn, **rs), out=self.hb)
       ops.gemm(self.hb, L.down, ops.epilogue(lib.EP_RESIDUAL, residual=self.x, ssq_out=self.ssq, copy_bf16=self.xn,

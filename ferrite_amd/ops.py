@@ -198,13 +198,15 @@ def attention_workspace(batch, heads, head_dim, max_context, device="cuda"):
 
 def attention_decode(q, cache, heads, kv_heads, head_dim, places, first_row, max_context, workspace, o=None):
   """softmax(q k^T / sqrt(hd)) v over each row's cache rows (fh_attention_decode). cache [2 kv][len][hd] (fp32, bf16 or
-  a BfpCache)."""
+  a BfpCache); o fp32 (by default) or bf16."""
   data, dtype, length = cache_fields(cache)
   _dev(q, data, places, first_row)
   batch = q.shape[0]
   if o is None: o = torch.empty_like(q)
-  lib.call("fh_attention_decode", _ptr(q), _ptr(data), dtype, length, batch, heads, kv_heads,
-           head_dim, _ptr(places), _ptr(first_row), max_context, _ptr(o), _ptr(workspace), workspace.numel(), _stream())
+  if o.dtype not in (torch.float32, torch.bfloat16) or o.shape != q.shape or not o.is_contiguous():
+    raise ValueError("attention_decode: o is a contiguous fp32 or bf16 tensor of q's shape")
+  lib.call("fh_attention_decode", _ptr(q), _ptr(data), dtype, length, batch, heads, kv_heads, head_dim, _ptr(places),
+           _ptr(first_row), max_context, _ptr(o), _TORCH[o.dtype], _ptr(workspace), workspace.numel(), _stream())
   return o
 
 

@@ -175,7 +175,8 @@ int fh_embed_rows(const void* table, int table_dtype, int64_t vocab, int64_t dim
 /* Decode attention over a KV cache (models/llama.py:129-142; Tensor.attend, ferrite/tensor.py:487-516): for each
  * row b and query head h, softmax(q k^T / sqrt(head_dim)) v over the cache rows first_row[b] .. first_row[b] +
  * places[b] (those its place reaches), k and v the heads of kv head h / (heads / kv_heads) (grouped-query).
- * q, o: [batch][heads*head_dim] fp32; heads / kv_heads at most 16. Flash decoding: the keys are shared out among
+ * q: [batch][heads*head_dim] fp32; o the same shape, fp32 or bf16 (o_dtype: rounded to nearest even, the rows the
+ * matrix-core matmuls take); heads / kv_heads at most 16. Flash decoding: the keys are shared out among
  * workgroups in chunks of 64 rows of one key head (each cache byte read once, for all the query heads that share it),
  * each writing its partial result and softmax statistics to the workspace, and a second kernel combines the chunks
  * by exp-weights (ferrite/compiler.py:1138-1145); a context of one chunk writes o directly. The workspace holds no
@@ -191,7 +192,7 @@ size_t fh_attention_workspace_bytes(int batch, int heads, int head_dim, int64_t 
 size_t fh_kv_cache_bytes(int cache_dtype, int kv_heads, int64_t cache_len, int head_dim);
 int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch, int heads,
                         int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row, int64_t max_context,
-                        float* o, void* workspace, size_t ws_bytes, void* stream);
+                        void* o, int o_dtype, void* workspace, size_t ws_bytes, void* stream);
 
 /* A prompt's causal attention (models/llama.py:129-142 over a chunk of consecutive places; prefill, 498-504): rows
  * t = 0 .. T-1 of q [T][ldq] (fp32) are places p0 + t of the sequence whose cache rows start at slot_row; row t

@@ -210,6 +210,11 @@ def test_attention_decode(cuda, hd, heads, kv):
     cv = cache if cd == torch.float32 else O.bf16(cache)
     o = ops().attention_decode(to_gpu(q), to_gpu(cache, cd), heads, kv, hd, to_gpu(places, torch.int32),
                                to_gpu(first, torch.int32), part, ws).cpu().numpy()
+    # o in bf16 (the matrix cores' rows): the fp32 result rounded to nearest even, bit for bit (one chunk, combined)
+    ob = torch.empty(q.shape, dtype=torch.bfloat16, device="cuda")
+    ops().attention_decode(to_gpu(q), to_gpu(cache, cd), heads, kv, hd, to_gpu(places, torch.int32),
+                           to_gpu(first, torch.int32), part, ws, o=ob)
+    assert torch.equal(ob.cpu(), torch.from_numpy(o).to(torch.bfloat16)), cd
     for b in range(batch):
       n = places[b] + 1
       k = np.repeat(cv[:kv, first[b]:first[b] + n], heads // kv, 0)
@@ -239,6 +244,8 @@ def test_attention_decode_many_rows(cuda, hd, heads, kv, batch, part):
   args = (heads, kv, hd, to_gpu(places, torch.int32), to_gpu(first, torch.int32), part, ws)
   for cd in (torch.bfloat16, torch.float32):
     o = ops().attention_decode(to_gpu(q), to_gpu(cache, cd), *args).cpu().numpy()
+    ob = ops().attention_decode(to_gpu(q), to_gpu(cache, cd), *args, o=torch.empty(q.shape, dtype=torch.bfloat16, device="cuda"))
+    assert torch.equal(ob.cpu(), torch.from_numpy(o).to(torch.bfloat16)), cd  # (bf16 o: fp32's rounded to nearest even)
     for b in range(batch):
       n = places[b] + 1
       k = np.repeat(cache[:kv, first[b]:first[b] + n], heads // kv, 0)
