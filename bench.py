@@ -208,12 +208,13 @@ def measured_traffic(kernel, config, batch):
   return None
 
 
-def cpu_baseline(c, mode, context, layers_timed=1):
+def cpu_baseline(c, mode, context, runs=5):
   """The numpy restatement (oracle/llama.py) of one decode token on this host: one block at the step's context plus the
-  output layer, each the median of 3 timed runs after a warm-up, the block's time scaled by c.layers. Float64 caches,
-  as models/llama.py's main makes them (activations promote to float64)."""
+  output layer, each the median of `runs` timed runs after a warm-up, the block's time scaled by c.layers. The value:
+  every core BLAS gives, float64 caches and activations as models/llama.py's main makes them (float32 weights promote);
+  beside it (medians of 3) the same on one BLAS thread, and with float32 activations and caches."""
+  from threadpoolctl import threadpool_limits, threadpool_info
   from oracle import llama as OL
-  from oracle import bfp as O
   rng = np.random.default_rng(0)
   hd = c.dim // c.heads
   oc = OL.model(dim=c.dim, heads=c.heads, kv=c.kv, layers=1, eps=c.eps, theta=c.theta, vocab=c.vocab, ffn=c.ffn,
@@ -223,29 +224,36 @@ def cpu_baseline(c, mode, context, layers_timed=1):
   for name, shape in (("qkv_proj", (c.dim, (c.heads + 2 * c.kv) * hd)), ("o_proj", (c.heads * hd, c.dim)),
                       ("gate_up_proj", (c.dim, 2 * c.ffn)), ("down_proj", (c.ffn, c.dim))):
     p[name] = rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)
+  head_w = rng.standard_normal((c.dim, c.vocab), dtype=np.float32) * np.float32(0.02)
   cos, sin, t = OL.rotary(oc, context)
-  cache = np.zeros((2 * c.kv, context, hd))
-  x = rng.standard_normal((1, c.dim))
   place = context - 1
   mask = OL.masked([place], context)
   tables = (cos[[place]], sin[[place]], t)
-  def block():
-    OL.layer(x, p, oc, tables, mask, cache, [place])
-  head_w = rng.standard_normal((c.dim, c.vocab), dtype=np.float32) * np.float32(0.02)
-  def head():
-    return OL.rms(x, p["input_layernorm"], oc) @ head_w
-  times = {}
-  for name, fn in (("block", block), ("head", head)):
-    fn()
-    ts = []
-    for _ in range(3):
-      t0 = time.perf_counter(); fn(); ts.append(time.perf_counter() - t0)
-    times[name] = statistics.median(ts)
-  per_token = times["block"] * c.layers + times["head"]
-  return dict(value=1.0 / per_token, unit="tokens/s", cores=len(os.sched_getaffinity(0)), kind="port",
-              sample=f"numpy oracle: 1 of {c.layers} blocks at context {context} + output layer, median of 3, block x{c.layers}; "
-                     f"float64 cache (activations float64), float32 weights",
-              block_s=times["block"], head_s=times["head"])
+
+  def per_token(dtype, runs=runs):
+    cache = np.zeros((2 * c.kv, context, hd), dtype)
+    x = rng.standard_normal((1, c.dim)).astype(dtype)
+    fns = {"block": lambda: OL.layer(x, p, oc, tables, mask, cache, [place]),
+           "head": lambda: OL.rms(x, p["input_layernorm"], oc) @ head_w}
+    times = {}
+    for name, fn in fns.items():
+      fn()
+      ts = []
+      for _ in range(runs):
+        t0 = time.perf_counter(); fn(); ts.append(time.perf_counter() - t0)
+      times[name] = statistics.median(ts)
+    return times["block"] * c.layers + times["head"], times
+
+  all64, times = per_token(np.float64)
+  all32, _ = per_token(np.float32, 3)
+  with threadpool_limits(limits=1, user_api="blas"):
+    one64, _ = per_token(np.float64, 3)
+  blas = [f"{i['internal_api']} {i['version']} x{i['num_threads']}" for i in threadpool_info() if i["user_api"] == "blas"]
+  return dict(value=1.0 / all64, unit="tokens/s", cores=len(os.sched_getaffinity(0)), kind="port",
+              sample=f"numpy oracle: 1 of {c.layers} blocks at context {context} + output layer, median of {runs}, block "
+                     f"x{c.layers}; float64 cache and activations (float32 weights), every core BLAS gives",
+              block_s=times["block"], head_s=times["head"], blas=", ".join(blas),
+              one_thread_tokens_per_s=1.0 / one64, float32_tokens_per_s=1.0 / all32)
 
 
 def main():
@@ -337,8 +345,11 @@ def main():
   cpu = None
   if not args.no_cpu:
     cpu = cpu_baseline(c, mode, context)
-    print(f"# cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} cores (block {cpu['block_s']:.3f}s, head {cpu['head_s']:.3f}s)", file=sys.stderr)
-    cpu = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
+    print(f"# cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} cores (block {cpu['block_s']:.3f}s, head "
+          f"{cpu['head_s']:.3f}s; {cpu['blas']}); one BLAS thread {cpu['one_thread_tokens_per_s']:.3f}, float32 "
+          f"activations and cache {cpu['float32_tokens_per_s']:.3f} tok/s", file=sys.stderr)
+    cpu = {k: (round(cpu[k], 4) if isinstance(cpu[k], float) else cpu[k])
+           for k in ("value", "unit", "cores", "kind", "sample", "blas", "one_thread_tokens_per_s", "float32_tokens_per_s")}
   line = {
     "metric": "8B-shape bfp8 decode tok/s @bs1; GEMV HBM GB/s as % of peak",
     "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
