@@ -208,6 +208,38 @@ def measured_traffic(kernel, config, batch):
   return None
 
 
+def measured_peaks(dev, reps=10):
+  """What this GPU reaches on plain library kernels, beside the published peaks: HBM read (torch.sum of 2 GiB of fp32
+  by rows of 1024, every byte read once: the fastest of the reductions tried, ~6.4 TB/s) and copy (torch.neg, 2 GiB in and out), and a large bf16 GEMM on the matrix cores
+  (torch.matmul, hipBLASLt, 8192^3), each timed by HIP events on the current stream after a warm-up."""
+  def timed(fn):
+    fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps): fn()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / reps * 1e-3
+  n = 1 << 29
+  src = torch.ones(n, device=dev)
+  dst = torch.empty_like(src)
+  rows = src.view(-1, 1024)
+  acc = torch.empty(rows.shape[0], device=dev)
+  read = 4 * n / timed(lambda: torch.sum(rows, 1, out=acc))
+  copy = 8 * n / timed(lambda: torch.neg(src, out=dst))
+  del src, dst
+  m = 8192
+  x = torch.randn(m, m, device=dev, dtype=torch.bfloat16)
+  w = torch.randn(m, m, device=dev, dtype=torch.bfloat16)
+  y = torch.empty(m, m, device=dev, dtype=torch.bfloat16)
+  gemm = 2 * m ** 3 / timed(lambda: torch.matmul(x, w, out=y))
+  del x, w, y
+  torch.cuda.empty_cache()
+  return {"hbm_read_gbs": round(read / 1e9, 1), "hbm_copy_gbs": round(copy / 1e9, 1),
+          "bf16_gemm_tflops": round(gemm / 1e12, 1)}
+
+
 def cpu_baseline(c, mode, context, runs=5):
   """The numpy restatement (oracle/llama.py) of one decode token on this host: one block at the step's context plus the
   output layer, each the median of `runs` timed runs after a warm-up, the block's time scaled by c.layers. The value:
@@ -310,6 +342,10 @@ def main():
   step_bytes = dec.weight_bytes() + kv_bytes
   print(f"# step {ms:.3f} ms, {tok_s:.1f} tok/s, {step_bytes / 1e9:.3f} GB a step -> {step_bytes / ms / 1e6:.0f} GB/s", file=sys.stderr, flush=True)
   rates = gemv_rates(dec, stream)
+  peaks = measured_peaks(dev)
+  print(f"# measured on this GPU: HBM read {peaks['hbm_read_gbs']:.0f} GB/s, copy {peaks['hbm_copy_gbs']:.0f} GB/s (published "
+        f"{HBM_PEAK / 1e9:.0f}); bf16 GEMM {peaks['bf16_gemm_tflops']:.0f} TFLOP/s (published dense {MFMA_PEAK / 1e12:.0f})",
+        file=sys.stderr, flush=True)
   for k, r in rates.items():
     print(f"# gemv {k:8s} {r['fmt']} {r['K']}x{r['N']}: {r['us']:.2f} us, {r['gbs']:.0f} GB/s ({r['gbs'] * 1e9 / HBM_PEAK:.1%})", file=sys.stderr, flush=True)
   rates8 = None
@@ -339,6 +375,7 @@ def main():
   pre = None
   if not args.no_prefill and args.config == "c3":
     pre = prefill_rate()
+    pre["mfma_frac_measured"] = round(pre["tflops"] / peaks["bf16_gemm_tflops"], 4)  # (of hipBLASLt's bf16 GEMM here)
     print(f"# prefill {pre['workload']}: {pre['ms']:.1f} ms, {pre['tokens_per_s']:.0f} tok/s, {pre['tflops']:.0f} TFLOP/s "
           f"({pre['mfma_frac']:.1%} of {MFMA_PEAK / 1e15:.1f} PFLOP/s); gemm {pre['gemm_tflops']}, attention {pre['attention_tflops']} TFLOP/s",
           file=sys.stderr, flush=True)
@@ -361,7 +398,9 @@ def main():
     "step_gbs": round(step_bytes / ms / 1e6, 1), "step_bytes": step_bytes,
     "roofline": {"bound": "hbm", "kernel": f"gemv {dom} + {epi[dom]} ({r['fmt']} {r['K']}x{r['N']})", "achieved": round(r["gbs"], 1),
                  "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(r["gbs"] * 1e9 / HBM_PEAK, 4),
-                 "traffic": measured_traffic(dom, args.config, B)},
+                 "traffic": measured_traffic(dom, args.config, B),
+                 "measured_peak": peaks["hbm_read_gbs"], "frac_measured": round(r["gbs"] / peaks["hbm_read_gbs"], 4)},
+    "measured_peaks": peaks,
     "gemv_gbs": {k: round(v["gbs"], 1) for k, v in rates.items()},
     "gemv_us": {k: round(v["us"], 3) for k, v in rates.items()},
     "gemv_bfp8_8b": None if rates8 is None else {k: {"us": round(v["us"], 3), "gbs": round(v["gbs"], 1),
