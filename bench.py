@@ -133,9 +133,9 @@ def prefill_rate(T=2048, reps=3):
 
 
 def decode_batch(dec, context, B=16, steps=20):
-  """Config 3 at batch 16: 16 sequences a step, each at the last place of a full context of its own (a slot of the
-  cache each), the matmuls on the matrix cores (the skinny kernel), the step replayed as a HIP graph; the weights are
-  the batch-1 decoder's."""
+  """Config 3 at batch B (16 by default): B sequences a step, each at the last place of a full context of its own (a
+  slot of the cache each), the matmuls on the matrix cores (the skinny kernel) from Decoder's mfma_from rows on, the
+  step replayed as a HIP graph; the weights are the batch-1 decoder's."""
   from ferrite_amd import llama as G
   c = dec.c
   d = G.Decoder(c, None, mode=dec.mode, kv="bf16", batch=B, context=context, slots=B, share=dec)
@@ -155,7 +155,8 @@ def decode_batch(dec, context, B=16, steps=20):
   ms = a.elapsed_time(b) / steps
   kv = c.layers * 2 * c.kv * d.hd * context * 2 * B
   nbytes = d.weight_bytes() + kv
-  out = {"workload": f"config 3 at batch {B}: {B} sequences at context {context}, matmuls on the matrix cores",
+  on = "the matrix cores" if d.mm.__name__ == "gemm" else "the GEMV"
+  out = {"workload": f"config 3 at batch {B}: {B} sequences at context {context}, matmuls on {on}",
          "batch": B, "ms_per_step": round(ms, 4), "tokens_per_s": round(B * 1000 / ms, 1),
          "step_gbs": round(nbytes / ms / 1e6, 1)}
   del d
@@ -364,6 +365,12 @@ def main():
   extra = {}
   if args.config == "c3" and B == 1 and not args.no_prefill:
     extra["decode_bs16"] = decode_batch(dec, context)
+    extra["decode_batches"] = {}
+    for nb in (2, 4, 8):  # (2 on the GEMV, 4 and 8 on the matrix cores: Decoder's mfma_from)
+      rb = decode_batch(dec, context, B=nb)
+      extra["decode_batches"][str(nb)] = {"ms_per_step": rb["ms_per_step"], "tokens_per_s": rb["tokens_per_s"]}
+    print("# decode at batch " + ", ".join(f"{nb}: {v['ms_per_step']:.3f} ms ({v['tokens_per_s']:.0f} tok/s)"
+                                           for nb, v in extra["decode_batches"].items()), file=sys.stderr, flush=True)
     print(f"# {extra['decode_bs16']['workload']}: {extra['decode_bs16']['ms_per_step']:.3f} ms, "
           f"{extra['decode_bs16']['tokens_per_s']:.0f} tok/s, {extra['decode_bs16']['step_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     extra["moe"] = moe_rate()

@@ -11,6 +11,7 @@
 // (about 60 a lane at batch 1) keep ~32 waves on every CU, each with its loads in flight: a decode GEMV is a
 // latency-bound stream, and that is what hides the latency. Nothing crosses workgroups: no atomics, no fences.
 #include <math.h>
+#include <algorithm>
 #include <type_traits>
 #include "fh_epilogue.h"
 
@@ -19,8 +20,11 @@ namespace fh {
 // rows a lane has in flight at once, by format and batch rows (about 4 KiB of weight a wave and run at batch 1)
 __host__ __device__ constexpr int gemv_group(bool four, int b, int p) { return (b <= 2 ? 4 : b <= 4 ? 2 : 1) * (four ? 2 : 1) + 0 * p; }
 
+// threads a workgroup at most: 16 waves for one row, 8 for more (whose partial sums need the registers)
+__host__ __device__ constexpr int gemv_threads(int b) { return b == 1 ? 1024 : 512; }
+
 template <bool FOUR, int B, int P, bool NORM>
-__global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
+__global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(MatArgs a) {
   constexpr int V = B * P * 16;       // a lane's partial sums: [b][p][j]
   constexpr int G = B * P;
   constexpr int U = gemv_group(FOUR, B, P);
@@ -108,7 +112,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(MatArgs a) {
     sums[gi] = r16[0];
   }
   const int j16 = reduce16_index(lane);
-  __shared__ float red[16][V];
+  __shared__ float red[gemv_threads(B) / 64][V];
   __shared__ float fin[V];
   if ((lane & 3) == 0) {
 #pragma unroll
@@ -235,7 +239,9 @@ static int dispatch_batch(const MatArgs& a, int batch, int items, int W, hipStre
 }
 
 // The K slices: W waves a workgroup, the least power of 2 giving about 16384 waves in all (64 a CU on 256 CUs, in
-// turns), at most one a group of U loads of 64 rows a lane, and at most 16 for bfp4 and 8 for bfp8: a bfp8 wave needs
+// turns), at most one a group of U loads of 64 rows a lane, at most 8 for more than one row (their launch bound is 512
+// threads, so that the rows' partial sums stay in registers: bound to 1024 threads they spilled, and batch 8 of an 8B
+// step took 35.6 ms instead of 6.5), and at most 16 for bfp4 and 8 for bfp8 at one row: a bfp8 wave needs
 // ~100 registers at two runs an item, so a 16-wave workgroup fills a CU alone and the grid runs in lock-step rounds
 // (on MI355X: the 8B shapes' bfp8 gate_up 31.7 us at 16, 25.9 at 8; bfp4's down 11.0 at 16, 11.4 at 8).
 struct Plan { int W, rows, P, most, items; };
@@ -247,7 +253,8 @@ static Plan plan(int64_t K, int64_t N, int fmt, int kind, int batch) {
   const int b = batch < p.most ? batch : p.most;
   const int unit = 64 * gemv_group(fmt == FH_BFP4, b, p.P);
   const int64_t units = (K + unit - 1) / unit;
-  const int64_t most = fmt == FH_BFP4 ? 16 : 8;  // (measured: bfp8's 16-wave workgroups run in lock-step rounds)
+  const int64_t most = std::min<int64_t>(fmt == FH_BFP4 ? 16 : 8, gemv_threads(b) / 64);  // (measured: bfp8's 16-wave
+                                                                                           // workgroups run in lock-step rounds)
   int64_t W = 1;
   while (W < most && W * p.items < 16384) W *= 2;
   while (W > 1 && W > units) W /= 2;
