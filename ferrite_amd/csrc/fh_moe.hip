@@ -315,15 +315,24 @@ extern "C" int fh_moe_route(const float* x, int64_t ldx, int rows, int64_t dim, 
 }
 
 // Rows a pass: up to 64 rows (a decode step's), one pass through the skinny kernel, each touched expert's weight read
-// once; past 64 (a prompt's), passes of up to 1024 through the tiled GEMM, an expert's weight read once for every 128
-// of its rows (models/llama.py:314-329: the touched path for a decode step, the group path past it; the reference
-// turns at 128 tokens, here the tiled GEMM is already faster from 65: 560 us against 680 for two skinny passes at the
-// Mixtral shape). A pass's workspace holds each expert's whole pass of rows (a `dense` may pick every expert for a
-// row): ~370 MB for 1024 rows at the Mixtral shape; passes of 2048 were 13% faster at 2048 tokens for twice that.
-static int64_t moe_pass(int64_t rows) { return rows > 64 ? 1024 : 64; }
+// once; past 64 (a prompt's), passes through the tiled GEMM, an expert's weight read once for every 128 of its rows
+// (models/llama.py:314-329: the touched path for a decode step, the group path past it; the reference turns at 128
+// tokens, here the tiled GEMM is already faster from 65: 560 us against 680 for two skinny passes at the Mixtral
+// shape). A pass's workspace holds each expert's whole pass of rows (a `dense` may pick every expert for a row), so a
+// pass is the most rows, a power of 2 from 2048 down to 128, whose workspace fits MOE_BUDGET: 2048 at the Mixtral
+// shape (~740 MB; 13% faster at 2048 tokens than passes of 1024), 128 for 256 experts of 2048 x 7168.
+constexpr int64_t MOE_BUDGET = (int64_t)1 << 30;
+static int64_t moe_pass(int64_t rows, int64_t experts, int64_t ffn, int64_t dim) {
+  if (rows <= 64) return 64;
+  int64_t p = 2048;
+  while (p > 128 && (int64_t)moe_space(p, experts, ffn, dim).total > MOE_BUDGET) p /= 2;
+  return p;
+}
 
 extern "C" size_t fh_moe_workspace_bytes(int rows, int experts, int64_t ffn, int64_t dim) {
-  const int64_t r = rows < moe_pass(rows) ? rows : moe_pass(rows);  // a pass's rows
+  if (rows < 1 || experts < 1 || ffn < 1 || dim < 1) return 0;
+  const int64_t pass = moe_pass(rows, experts, ffn, dim);
+  const int64_t r = rows < pass ? rows : pass;  // a pass's rows
   if (r < 1 || experts < 1 || ffn < 1 || dim < 1) return 0;
   return moe_space(r, experts, ffn, dim).total;
 }
@@ -346,7 +355,7 @@ extern "C" int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim
   if (int rc = fh_bfp_bytes(dim, gu_n, gu_fmt, FH_AXIS_N, &mb, &eb)) return rc;
   size_t dmb, deb;
   if (int rc = fh_bfp_bytes(ffn, dim, down_fmt, FH_AXIS_N, &dmb, &deb)) return rc;
-  const int pass = (int)moe_pass(rows);
+  const int pass = (int)moe_pass(rows, experts, ffn, dim);
   for (int r0 = 0; r0 < rows; r0 += pass) {
     const int n = rows - r0 < pass ? rows - r0 : pass;
     const MoeSpace m = moe_space(n, experts, ffn, dim);

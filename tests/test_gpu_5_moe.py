@@ -51,12 +51,14 @@ def test_route(cuda, E, k, norm_topk):
   assert np.abs(dense.cpu().numpy() - d).max() <= bound
 
 
-@pytest.mark.parametrize("T,fmt", [(32, "bfp4"), (5, "bfp8"), (64, "bfp4"), (100, "bfp4"), (300, "bfp4"), (1100, "bfp8")])
+@pytest.mark.parametrize("T,fmt", [(32, "bfp4"), (5, "bfp8"), (64, "bfp4"), (100, "bfp4"), (300, "bfp4"),
+                                   (2200, "bfp8"), (2100, "bfp4")])
 def test_experts(cuda, T, fmt):
   # benchmark config 5's shape at a smaller width: 8 experts, top 2, the tokens' SwiGLUs weighted and summed onto the
   # residual; up to 64 tokens one pass through the skinny kernel; past that (models/llama.py:314-329's group path)
-  # passes of up to 1024 through the tiled GEMM, each expert's gathered rows a layer of the grid: 100 and 300 in one
-  # pass, 1100 in a pass of 1024 and one of 76
+  # passes of up to 2048 through the tiled GEMM (as many as the workspace budget allows: 2048 at this width), each
+  # expert's gathered rows a layer of the grid: 100 and 300 in one pass, 2200 in a pass of 2048 and one of 152, 2100
+  # in a pass of 2048 and one of 52 (through the skinny kernel)
   rng = np.random.default_rng(42)
   dim, ffn, E, k = 256, 512, 8, 2
   c = OL.model(dim=dim, eps=1e-5, k=k, experts=E)
