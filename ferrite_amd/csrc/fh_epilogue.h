@@ -86,8 +86,10 @@ struct SkinnyMoe {
   const float* row_scale; int experts;
   int scale_rows;
   // gathered (counts set): expert e takes counts[e] rows (at most M); its x row r is row x_rows[e M + r] of x (row
-  // e M + r where x_rows is null), its output row r is y's row e M + r, and (scale_rows) its scale row_w[e M + r]
+  // e M + r where x_rows is null), its output row r is y's row e M + r, and (scale_rows) its scale row_w[e M + r];
+  // a launch takes the expert's rows row0 .. row0 + 16 MB - 1 of those
   const int32_t* counts; const int32_t* x_rows; const float* row_w;
+  int row0;
 };
 
 // x @ W for up to 64 rows a pass on the matrix cores (fh_skinny.hip); a's epilogue already checked

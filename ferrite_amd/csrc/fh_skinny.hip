@@ -53,12 +53,14 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   const int item = blockIdx.x, e = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), W = blockDim.x >> 6;
   const bool gathered = moe.counts != nullptr;
-  const int M = gathered ? min(moe.counts[e], (int)a.M) : (int)a.M, K = (int)a.K;
+  // (gathered: this launch's rows of the expert, from row0 of its list)
+  const int M = gathered ? max(0, min(moe.counts[e], (int)a.M) - moe.row0) : (int)a.M, K = (int)a.K;
+  const int64_t list0 = gathered ? (int64_t)e * a.M + moe.row0 : 0;
   // a row's place in x and in y (gathered: the expert's own rows)
   auto xrow = [&](int r) -> int64_t {
-    return gathered ? (moe.x_rows ? moe.x_rows[(int64_t)e * a.M + r] : (int64_t)e * a.M + r) : r;
+    return gathered ? (moe.x_rows ? moe.x_rows[list0 + r] : list0 + r) : r;
   };
-  const int64_t yrow0 = gathered ? (int64_t)e * a.M : 0;
+  const int64_t yrow0 = list0;
 
   // the rows' weights for this expert; an expert no row picked writes its zeros and reads nothing
   if (t == 0) any_s = gathered ? M > 0 : (moe.row_scale ? 0 : 1);
@@ -66,7 +68,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   if (t < 16 * MB) {
     float sc = 1.f;
     if (gathered) {
-      if (moe.scale_rows) sc = t < M ? moe.row_w[(int64_t)e * a.M + t] : 0.f;
+      if (moe.scale_rows) sc = t < M ? moe.row_w[list0 + t] : 0.f;
     } else if (moe.row_scale) {
       const float r = t < M ? moe.row_scale[(int64_t)t * moe.experts + e] : 0.f;
       if (r != 0.f) any_s = 1;
@@ -358,8 +360,36 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
   const int items = (int)(one ? a0.N / 16 : a0.P == 1 ? (a0.N / 16 + 1) / 2 : a0.items);
   if (experts > 256) return fail(FH_EUNSUP, "skinny matmul: at most 256 experts");
   int W, rows;
-  const int mb0 = a0.M > 32 ? 4 : a0.M > 16 ? 2 : 1;
+  // gathered (an expert's rows through a list), launches of one 16-row block each: most experts have few rows, and an
+  // expert with none in a launch's block reads nothing (two blocks for 32 rows a pass took 158 registers a lane)
+  const bool gathered = moe.counts != nullptr;
+  const int mb0 = gathered ? 1 : a0.M > 32 ? 4 : a0.M > 16 ? 2 : 1;
   skinny_plan(a0.K, items, experts, skinny_threads(a0.x_bf16, mb0) / 64, W, rows);
+  auto launch = [&](const MatArgs& a, const SkinnyMoe& mo, int mb) {
+    const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
+    switch (which) {
+      case 0: skinny_runs<false, false, false>(a, mo, one, items, experts, W, mb, s); break;
+      case 1: skinny_runs<false, false, true>(a, mo, one, items, experts, W, mb, s); break;
+      case 2: skinny_runs<false, true, false>(a, mo, one, items, experts, W, mb, s); break;
+      case 3: skinny_runs<false, true, true>(a, mo, one, items, experts, W, mb, s); break;
+      case 4: skinny_runs<true, false, false>(a, mo, one, items, experts, W, mb, s); break;
+      case 5: skinny_runs<true, false, true>(a, mo, one, items, experts, W, mb, s); break;
+      case 6: skinny_runs<true, true, false>(a, mo, one, items, experts, W, mb, s); break;
+      default: skinny_runs<true, true, true>(a, mo, one, items, experts, W, mb, s); break;
+    }
+    return check_launch("skinny matmul");
+  };
+  if (gathered) {
+    if (a0.M > 64) return fail(FH_EUNSUP, "skinny matmul: at most 64 gathered rows an expert");
+    for (int r0 = 0; r0 < a0.M; r0 += 16) {
+      MatArgs a = a0;
+      a.rows = rows;
+      SkinnyMoe mo = moe;
+      mo.row0 = r0;
+      if (int rc = launch(a, mo, 1)) return rc;
+    }
+    return FH_OK;
+  }
   for (int64_t m0 = 0; m0 < a0.M; m0 += 64) {
     MatArgs a = a0;
     a.M = a0.M - m0 < 64 ? a0.M - m0 : 64;
@@ -375,18 +405,7 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
     SkinnyMoe mo = moe;
     if (mo.row_scale) mo.row_scale += m0 * mo.experts;
     const int mb = a.M > 32 ? 4 : a.M > 16 ? 2 : 1;
-    const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
-    switch (which) {
-      case 0: skinny_runs<false, false, false>(a, mo, one, items, experts, W, mb, s); break;
-      case 1: skinny_runs<false, false, true>(a, mo, one, items, experts, W, mb, s); break;
-      case 2: skinny_runs<false, true, false>(a, mo, one, items, experts, W, mb, s); break;
-      case 3: skinny_runs<false, true, true>(a, mo, one, items, experts, W, mb, s); break;
-      case 4: skinny_runs<true, false, false>(a, mo, one, items, experts, W, mb, s); break;
-      case 5: skinny_runs<true, false, true>(a, mo, one, items, experts, W, mb, s); break;
-      case 6: skinny_runs<true, true, false>(a, mo, one, items, experts, W, mb, s); break;
-      default: skinny_runs<true, true, true>(a, mo, one, items, experts, W, mb, s); break;
-    }
-    if (int rc = check_launch("skinny matmul")) return rc;
+    if (int rc = launch(a, mo, mb)) return rc;
   }
   return FH_OK;
 }
