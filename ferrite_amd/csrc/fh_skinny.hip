@@ -53,9 +53,11 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   const int item = blockIdx.x, e = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), W = blockDim.x >> 6;
   const bool gathered = moe.counts != nullptr;
-  // (gathered: this launch's rows of the expert, from row0 of its list)
-  const int M = gathered ? max(0, min(moe.counts[e], (int)a.M) - moe.row0) : (int)a.M, K = (int)a.K;
-  const int64_t list0 = gathered ? (int64_t)e * a.M + moe.row0 : 0;
+  // (gathered: this workgroup's rows of the expert, from row0 of its list: the launch's first, then 16 MB a layer of
+  // the grid's third dimension)
+  const int row0 = moe.row0 + 16 * MB * (int)blockIdx.z;
+  const int M = gathered ? max(0, min(moe.counts[e], (int)a.M) - row0) : (int)a.M, K = (int)a.K;
+  const int64_t list0 = gathered ? (int64_t)e * a.M + row0 : 0;
   // a row's place in x and in y (gathered: the expert's own rows)
   auto xrow = [&](int r) -> int64_t {
     return gathered ? (moe.x_rows ? moe.x_rows[list0 + r] : list0 + r) : r;
@@ -339,8 +341,9 @@ static void skinny_plan(int64_t K, int items, int experts, int most, int& W, int
 }
 
 template <bool FOUR, bool XBF16, bool NORM, int R>
-static void skinny_launch(const MatArgs& a, const SkinnyMoe& moe, int items, int experts, int W, int mb, hipStream_t s) {
-  const dim3 g(items, experts), b(64 * W);
+static void skinny_launch(const MatArgs& a, const SkinnyMoe& moe, int items, int experts, int W, int mb, int blocks,
+                          hipStream_t s) {
+  const dim3 g(items, experts, blocks), b(64 * W);
   const size_t lds = (size_t)(W + 1) * 16 * mb * 33 * 4;  // the sums' tiles (they reuse the weight tiles)
   const size_t tiles = (size_t)W * SK_TILE * 2;
   const size_t bytes = lds > tiles ? lds : tiles;
@@ -350,9 +353,10 @@ static void skinny_launch(const MatArgs& a, const SkinnyMoe& moe, int items, int
 }
 
 template <bool FOUR, bool XBF16, bool NORM>
-static void skinny_runs(const MatArgs& a, const SkinnyMoe& moe, bool one, int items, int experts, int W, int mb, hipStream_t s) {
-  if (one) skinny_launch<FOUR, XBF16, NORM, 1>(a, moe, items, experts, W, mb, s);
-  else skinny_launch<FOUR, XBF16, NORM, 2>(a, moe, items, experts, W, mb, s);
+static void skinny_runs(const MatArgs& a, const SkinnyMoe& moe, bool one, int items, int experts, int W, int mb,
+                        int blocks, hipStream_t s) {
+  if (one) skinny_launch<FOUR, XBF16, NORM, 1>(a, moe, items, experts, W, mb, blocks, s);
+  else skinny_launch<FOUR, XBF16, NORM, 2>(a, moe, items, experts, W, mb, blocks, s);
 }
 
 // M rows (at most 64 a pass) of a [grouped] skinny matmul; the caller checked the epilogue
@@ -363,35 +367,34 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
   const int items = (int)(one ? a0.N / 16 : a0.P == 1 ? (a0.N / 16 + 1) / 2 : a0.items);
   if (experts > 256) return fail(FH_EUNSUP, "skinny matmul: at most 256 experts");
   int W, rows;
-  // gathered (an expert's rows through a list), launches of one 16-row block each: most experts have few rows, and an
-  // expert with none in a launch's block reads nothing (two blocks for 32 rows a pass took 158 registers a lane)
+  // gathered (an expert's rows through a list): one 16-row block a workgroup, the blocks a layer each of the grid's
+  // third dimension: most experts have few rows, and an expert with none in a workgroup's block reads nothing (two
+  // blocks a workgroup for 32 rows a pass took 158 registers a lane; a launch a block spent ~9-13 us a launch on grids
+  // of workgroups that all exit at once)
   const bool gathered = moe.counts != nullptr;
   const int mb0 = gathered ? 1 : a0.M > 32 ? 4 : a0.M > 16 ? 2 : 1;
   skinny_plan(a0.K, items, experts, skinny_threads(a0.x_bf16, mb0) / 64, W, rows);
-  auto launch = [&](const MatArgs& a, const SkinnyMoe& mo, int mb) {
+  auto launch = [&](const MatArgs& a, const SkinnyMoe& mo, int mb, int blocks) {
     const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
     switch (which) {
-      case 0: skinny_runs<false, false, false>(a, mo, one, items, experts, W, mb, s); break;
-      case 1: skinny_runs<false, false, true>(a, mo, one, items, experts, W, mb, s); break;
-      case 2: skinny_runs<false, true, false>(a, mo, one, items, experts, W, mb, s); break;
-      case 3: skinny_runs<false, true, true>(a, mo, one, items, experts, W, mb, s); break;
-      case 4: skinny_runs<true, false, false>(a, mo, one, items, experts, W, mb, s); break;
-      case 5: skinny_runs<true, false, true>(a, mo, one, items, experts, W, mb, s); break;
-      case 6: skinny_runs<true, true, false>(a, mo, one, items, experts, W, mb, s); break;
-      default: skinny_runs<true, true, true>(a, mo, one, items, experts, W, mb, s); break;
+      case 0: skinny_runs<false, false, false>(a, mo, one, items, experts, W, mb, blocks, s); break;
+      case 1: skinny_runs<false, false, true>(a, mo, one, items, experts, W, mb, blocks, s); break;
+      case 2: skinny_runs<false, true, false>(a, mo, one, items, experts, W, mb, blocks, s); break;
+      case 3: skinny_runs<false, true, true>(a, mo, one, items, experts, W, mb, blocks, s); break;
+      case 4: skinny_runs<true, false, false>(a, mo, one, items, experts, W, mb, blocks, s); break;
+      case 5: skinny_runs<true, false, true>(a, mo, one, items, experts, W, mb, blocks, s); break;
+      case 6: skinny_runs<true, true, false>(a, mo, one, items, experts, W, mb, blocks, s); break;
+      default: skinny_runs<true, true, true>(a, mo, one, items, experts, W, mb, blocks, s); break;
     }
     return check_launch("skinny matmul");
   };
   if (gathered) {
     if (a0.M > 64) return fail(FH_EUNSUP, "skinny matmul: at most 64 gathered rows an expert");
-    for (int r0 = 0; r0 < a0.M; r0 += 16) {
-      MatArgs a = a0;
-      a.rows = rows;
-      SkinnyMoe mo = moe;
-      mo.row0 = r0;
-      if (int rc = launch(a, mo, 1)) return rc;
-    }
-    return FH_OK;
+    MatArgs a = a0;
+    a.rows = rows;
+    SkinnyMoe mo = moe;
+    mo.row0 = 0;
+    return launch(a, mo, 1, (int)((a0.M + 15) / 16));
   }
   for (int64_t m0 = 0; m0 < a0.M; m0 += 64) {
     MatArgs a = a0;
@@ -408,7 +411,7 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
     SkinnyMoe mo = moe;
     if (mo.row_scale) mo.row_scale += m0 * mo.experts;
     const int mb = a.M > 32 ? 4 : a.M > 16 ? 2 : 1;
-    if (int rc = launch(a, mo, mb)) return rc;
+    if (int rc = launch(a, mo, mb, 1)) return rc;
   }
   return FH_OK;
 }
