@@ -90,3 +90,30 @@ def test_experts(cuda, T, fmt):
   want0 = d0 * (OL.glu(gu[:, :ffn], gu[:, ffn:]) @ q["experts.down"][0])
   if np.abs(want0).max() > 0: north_star(y0, want0, ("expert 0 alone", T))
   else: assert not y0.any()
+
+
+@pytest.mark.parametrize("T", [17, 64])
+def test_experts_every_row_on_two_experts(cuda, T):
+  # every token picks the same two experts (positive rows, a router whose columns 3 and 5 dominate for all of them), so
+  # those experts' gathered lists hold all T rows: 2 (17 tokens) and 4 (64 tokens) blocks of 16 rows through the
+  # skinny kernel's third grid dimension, the last one partial at 17; the other six experts take no row
+  rng = np.random.default_rng(7)
+  dim, ffn, E, k = 256, 512, 8, 2
+  c = OL.model(dim=dim, eps=1e-5, k=k, experts=E)
+  x = np.abs(rng.normal(0, 1, (T, dim))).astype(np.float32) + 0.1
+  g = O.bf16(rng.normal(1, 0.1, (1, dim)))
+  ssq = (x.reshape(T, -1, 16) ** 2).sum(-1).astype(np.float32)
+  router = rng.normal(0, 0.01, (dim, E))
+  router[:, 3] += 0.05
+  router[:, 5] += 0.04
+  p = {"router": O.bf16(router), "experts.gate_up": rng.normal(0, 0.05, (E, dim, 2 * ffn)).astype(np.float32),
+       "experts.down": rng.normal(0, 0.05, (E, ffn, dim)).astype(np.float32)}
+  q = {"router": p["router"], "experts.gate_up": O.bfp(p["experts.gate_up"], "bfp4"), "experts.down": O.bfp(p["experts.down"], "bfp4")}
+  h = OL.rms(x.astype(np.float64), g, c)
+  want, want_ids, want_w = OL.moe(h, q, c)
+  assert (np.sort(want_ids, axis=1) == [3, 5]).all()
+  ex = ops().pack_experts(to_gpu(p["experts.gate_up"]), to_gpu(p["experts.down"]), "bfp4")
+  ids, w, dense = ops().moe_route(to_gpu(x), to_gpu(p["router"], torch.bfloat16), E, k, True, norm_w=to_gpu(g.reshape(-1)), eps=c.eps)
+  assert np.array_equal(ids.cpu().numpy(), want_ids)
+  y = ops().moe_experts(to_gpu(x), ex, dense, norm_w=to_gpu(g.reshape(-1)), ssq_in=to_gpu(ssq), eps=c.eps)
+  north_star(y.cpu().numpy(), want, ("two experts take every row", T))
