@@ -7,7 +7,7 @@ Prints ONE JSON line: tokens/s of the whole decode step (every kernel of it repl
 in HBM), the dominant GEMV's achieved HBM bandwidth against the 8 TB/s peak (timed live with HIP events on its own
 stream), each GEMV's GB/s, and the CPU baseline: the numpy restatement (oracle/) of one block and the output layer
 timed on this host's cores and scaled to a token; and config 4's prefill (a 2048-token prompt on the matrix cores) as
-its own field. Synthetic data: random-init weights, drawn on the GPU and packed there."""
+its own field, with the same step with every matrix bfp8 (`decode_bfp8`), batches 2-16, and config 5's MoE layer. Synthetic data: random-init weights, drawn on the GPU and packed there."""
 import argparse, json, os, statistics, sys, time
 import numpy as np
 import torch
@@ -80,6 +80,29 @@ def gemv_rates(dec, stream, reps=5):
     nbytes = w.nbytes + B * w.K * 4 + B * y.shape[1] * 4 + extra  # W, x, y (and the norm's weights)
     out[name] = dict(fmt=w.fmt, K=w.K, N=w.N, bytes=nbytes, us=per * 1e6, gbs=nbytes / per / 1e9)
   return out
+
+
+def step_rate(dec, context, steps, warmup, stream):
+  """A batch-1 decoder's whole step at the last place of a full context of random keys and values, captured as one
+  HIP graph and replayed `steps` times between two HIP events on `stream` (as main times config 3's step)."""
+  c = dec.c
+  for cache in dec.cache: cache.normal_(0, 1)
+  with torch.cuda.stream(stream):
+    dec.ids.copy_(torch.tensor([1], dtype=torch.int32))
+    dec.set_rows([context - 1], [0])
+    dec.step(replay=True)
+    for _ in range(warmup): dec.graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps): dec.graph.replay()
+    b.record(stream)
+    b.synchronize()
+  ms = a.elapsed_time(b) / steps
+  nbytes = dec.weight_bytes() + c.layers * 2 * c.kv * dec.hd * context * 2
+  return {"workload": f"config 3 with every matrix bfp8: Llama-3.1-8B-shape decode, batch 1, context {context}, bf16 KV",
+          "ms_per_step": round(ms, 4), "tokens_per_s": round(1000 / ms, 2), "step_bytes": nbytes,
+          "step_gbs": round(nbytes / ms / 1e6, 1)}
 
 
 def prefill_rate(T=2048, reps=3):
@@ -350,9 +373,13 @@ def main():
   for k, r in rates.items():
     print(f"# gemv {k:8s} {r['fmt']} {r['K']}x{r['N']}: {r['us']:.2f} us, {r['gbs']:.0f} GB/s ({r['gbs'] * 1e9 / HBM_PEAK:.1%})", file=sys.stderr, flush=True)
   rates8 = None
+  extra = {}
   if args.config == "c3" and B == 1:  # the target's own kernels: the 8B shapes with every matrix bfp8
     c8, mode8, _ = config("c3-bfp8")
-    dec8 = G.Decoder(c8, G.random_weights(c8, seed=2, device=dev), mode=mode8, kv="bf16", batch=1, context=8)
+    dec8 = G.Decoder(c8, G.random_weights(c8, seed=2, device=dev), mode=mode8, kv="bf16", batch=1, context=context)
+    extra["decode_bfp8"] = step_rate(dec8, context, args.steps, args.warmup, stream)
+    print(f"# {extra['decode_bfp8']['workload']}: {extra['decode_bfp8']['ms_per_step']:.3f} ms, "
+          f"{extra['decode_bfp8']['tokens_per_s']:.1f} tok/s, {extra['decode_bfp8']['step_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     rates8 = gemv_rates(dec8, stream)
     for k, r8 in rates8.items():
       print(f"# gemv all-bfp8 {k:8s} {r8['fmt']} {r8['K']}x{r8['N']}: {r8['us']:.2f} us, {r8['gbs']:.0f} GB/s "
@@ -362,7 +389,6 @@ def main():
   dom = max(rates, key=lambda k: rates[k]["us"] * (c.layers if k != "head" else 1))  # the most time in a step
   r = rates[dom]
   epi = {"qkv": "RMSNorm+RoPE+KV put", "o": "residual", "gate_up": "RMSNorm+SiLU*gate", "down": "residual", "head": "RMSNorm+argmax"}
-  extra = {}
   if args.config == "c3" and B == 1 and not args.no_prefill:
     extra["decode_bs16"] = decode_batch(dec, context)
     extra["decode_batches"] = {}

@@ -572,12 +572,16 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   // S: workgroups a (row, key head), enough that the grid fills every CU as far as LDS and waves let it (all of it
   // resident at once, each workgroup walking its chunks), at most the launch's chunks; with one chunk a workgroup, q
   // is staged in LDS with the chunk (its scalar loads would wait behind the chunk's)
-  static int cus = 0, lds_cu = 0;
-  if (!cus) {
+  // (the first call's device, read once: a function-local static is initialised once whatever the threads calling)
+  struct CuShape { int cus, lds_cu; };
+  static const CuShape shape = [] {
+    CuShape c = {0, 0};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
-    if (hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || lds_cu < 65536) lds_cu = 160 * 1024;
-  }
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&c.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c.cus < 1) c.cus = 256;
+    if (hipDeviceGetAttribute(&c.lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || c.lds_cu < 65536) c.lds_cu = 160 * 1024;
+    return c;
+  }();
+  const int cus = shape.cus, lds_cu = shape.lds_cu;
   const int es = cache_dtype == FH_F32 ? 4 : 2;
   const int64_t pairs = (int64_t)kv_heads * batch;
   auto splits_for = [&](int64_t lds_bytes, int64_t waves) {

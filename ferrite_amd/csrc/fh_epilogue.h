@@ -87,7 +87,8 @@ struct SkinnyMoe {
   int scale_rows;
   // gathered (counts set): expert e takes counts[e] rows (at most M); its x row r is row x_rows[e M + r] of x (row
   // e M + r where x_rows is null), its output row r is y's row e M + r, and (scale_rows) its scale row_w[e M + r];
-  // a launch takes the expert's rows row0 .. row0 + 16 MB - 1 of those
+  // a workgroup takes the expert's rows row0 + 16 MB z .. row0 + 16 MB z + 16 MB - 1 of those, z its layer of the
+  // grid's third dimension
   const int32_t* counts; const int32_t* x_rows; const float* row_w;
   int row0;
 };
