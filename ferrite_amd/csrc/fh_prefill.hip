@@ -208,19 +208,43 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(const float* x, int64_t l
                                                        int centered, void* out, int64_t ldo) {
   const int64_t row = blockIdx.x;
   const float* xr = x + row * ldx;
+  __shared__ float part[4];
+  auto put = [&](int i, float xi, float rs) {
+    const float g = centered ? w[i] + 1.f : w[i];
+    const float v = xi * rs * g;
+    if (OBF16) ((uint16_t*)out)[row * ldo + i] = (uint16_t)bf16_rne_f(v);
+    else ((float*)out)[row * ldo + i] = v;
+  };
+  constexpr int R = 16;  // values a thread holds for a row of up to 256 R: all its loads issued at once, read once
+  if (dim <= 256 * R) {
+    float xv[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int i = threadIdx.x + 256 * j;
+      xv[j] = xr[i < dim ? i : 0];
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      if (threadIdx.x + 256 * j < dim) s += xv[j] * xv[j];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float rs = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)dim + eps);
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int i = threadIdx.x + 256 * j;
+      if (i < dim) put(i, xv[j], rs);
+    }
+    return;
+  }
   float s = 0.f;
   for (int i = threadIdx.x; i < dim; i += 256) s += xr[i] * xr[i];
   s = wave_sum(s);
-  __shared__ float part[4];
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
   __syncthreads();
   const float rs = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)dim + eps);
-  for (int i = threadIdx.x; i < dim; i += 256) {
-    const float g = centered ? w[i] + 1.f : w[i];
-    const float v = xr[i] * rs * g;
-    if (OBF16) ((uint16_t*)out)[row * ldo + i] = (uint16_t)bf16_rne_f(v);
-    else ((float*)out)[row * ldo + i] = v;
-  }
+  for (int i = threadIdx.x; i < dim; i += 256) put(i, xr[i], rs);
 }
 
 template <int HD>

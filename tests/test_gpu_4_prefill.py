@@ -78,11 +78,14 @@ def test_attention_prefill_rejects(cuda):
     ops().attention_prefill(torch.zeros(8, 96, device="cuda"), torch.zeros(2, 10, 96, device="cuda"), 1, 1, 96, 0, 0)
 
 
-def test_rms_rows(cuda):
+@pytest.mark.parametrize("dim", [576, 4096, 5000])
+def test_rms_rows(cuda, dim):
+  # a row of up to 4096 values held in registers (576: a partial last round of 256; 4096: all 16 rounds full), past
+  # that the row read twice (5000)
   rng = np.random.default_rng(33)
-  c = OL.model(dim=576, eps=1e-5)
-  x = rng.normal(0, 3, (37, 576)).astype(np.float32)
-  w = O.bf16(rng.normal(1, 0.1, (1, 576)))
+  c = OL.model(dim=dim, eps=1e-5)
+  x = rng.normal(0, 3, (37, dim)).astype(np.float32)
+  w = O.bf16(rng.normal(1, 0.1, (1, dim)))
   for centered in (False, True):
     c.centered = centered
     want = OL.rms(x.astype(np.float64), w, c)
