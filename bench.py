@@ -59,7 +59,7 @@ def gemv_rates(dec, stream, reps=5):
   c, B = dec.c, dec.batch
   calls = {
     "qkv": [(dec.x, L.qkv, lambda L=L, l=l: ops.epilogue(lib.EP_ROPE_KV, norm_w=L.norm1, ssq_in=dec.ssq, eps=c.eps, heads=c.heads,
-             kv_heads=c.kv, head_dim=dec.hd, cos_tab=dec.cos, sin_tab=dec.sin, places=dec.places, cache_rows=dec.rows,
+             kv_heads=c.kv, head_dim=dec.hd, cos_tab=dec.cos, sin_tab=dec.sin, rope_rows=dec.cos.shape[0], places=dec.places, cache_rows=dec.rows,
              **dec._cache(l)), dec.q, c.dim * 4)
             for l, L in enumerate(dec.layers)],
     "o": [(dec.att, L.o, lambda: ops.epilogue(lib.EP_RESIDUAL, residual=dec.x, ssq_out=dec.ssq), dec.x, 0) for L in dec.layers],

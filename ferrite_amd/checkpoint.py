@@ -25,11 +25,22 @@ def _json(path):
 
 
 def config(folder, places=4096):
-  """The model of a checkpoint's config.json (models/llama.py:541-570 for the models this path runs: Llama, Mistral,
-  SmolLM, Qwen2/3-style and Mixtral-style blocks; RoPE plain or Llama 3's scaling). places: the most places RoPE's
-  tables need rows for (at most the model's)."""
+  """The model of a checkpoint's config.json (models/llama.py:541-570) for the blocks this path runs: Llama's, SmolLM's,
+  Mistral's (where its sliding window covers every place the tables hold) and Mixtral's; RoPE plain or with Llama 3's
+  scaling. places: the most places RoPE's tables need rows for (at most the model's). What it cannot run raises
+  NotImplementedError rather than loading into wrong logits: a sliding window shorter than the places, Qwen3.5's
+  gated and linear-attention blocks, a shared expert, dense blocks among a mixture's, gpt-oss's clamped GLU (and, in
+  Checkpoint, the tensors of Qwen2's q/k/v biases, Qwen3's q/k norms, gpt-oss's sinks and o_proj bias)."""
   j = _json(os.path.join(folder, "config.json"))
   j = j.get("text_config", j)
+  window = j.get("sliding_window") if j.get("use_sliding_window", True) else None
+  if window and window < min(j["max_position_embeddings"], places):
+    raise NotImplementedError(f"checkpoint: a sliding window of {window} places (attention here sees every place)")
+  unsupported = [k for k in ("layer_types", "attn_output_gate", "linear_conv_kernel_dim", "shared_expert_intermediate_size",
+                             "swiglu_limit", "mlp_only_layers") if j.get(k)]
+  if j.get("decoder_sparse_step", 1) != 1: unsupported.append("decoder_sparse_step")
+  if j.get("model_type", "").startswith(("qwen3_5", "qwen3_next", "gpt_oss")): unsupported.append(f"model_type {j['model_type']}")
+  if unsupported: raise NotImplementedError(f"checkpoint: {', '.join(unsupported)} (not on this path)")
   rope = dict(j.get("rope_parameters") or (j.get("rope_scaling") or {}) | {"rope_theta": j["rope_theta"]})
   theta, kind = rope.pop("rope_theta"), rope.pop("type", None)
   rope.setdefault("rope_type", kind or "default")
@@ -82,6 +93,9 @@ class Checkpoint:
         if t["dtype"] not in ("BF16", "F32"): raise NotImplementedError(f"checkpoint: {full} is {t['dtype']} (BF16 or F32)")
         self.tensors[_name(full)] = (data, t)
     if "embed_tokens" not in self.tensors: raise ValueError("checkpoint: no embed_tokens")
+    extra = sorted(n for n in self.tensors if n.endswith(("q_proj.bias", "k_proj.bias", "v_proj.bias", "o_proj.bias", "q_norm",
+                                                          "k_norm", "sinks")))
+    if extra: raise NotImplementedError(f"checkpoint: {extra[0]} and the like (biases, q/k norms, sinks) are not on this path")
 
   def shape(self, name):
     return tuple(self.tensors[name][1]["shape"])

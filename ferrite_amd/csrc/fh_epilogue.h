@@ -13,6 +13,8 @@ struct MatArgs {
   int pair_half;            // P == 2: the runs of a pair are nb0 and nb0 + pair_half
   int items;                // N / 16 / P
   int rows;                 // GEMV: K in slices of `rows` rows (a multiple of 64), one a wave
+  int64_t row_base;         // the launch's first row among the call's (a call of many rows in several launches): the
+                            // row an FH_EP_PROGRAM input is read at
   // prologue
   const float* norm_w; const float* ssq_in; int ssq_parts; float eps; int centered;
   // epilogue
@@ -21,7 +23,7 @@ struct MatArgs {
   const float* residual; float* ssq_out; uint16_t* copy_bf16; const float* copy_w;
   int split;
   int heads, kv_heads, head_dim;
-  const float* cos_tab; const float* sin_tab; const int32_t* places; const int32_t* cache_rows;
+  const float* cos_tab; const float* sin_tab; int64_t rope_rows; const int32_t* places; const int32_t* cache_rows;
   void* cache; int cache_fmt; int64_t cache_len; uint8_t* cache_exps;  // (cache_exps: a block float's exponents)
   int2* argmax_parts;
   fh_program prog;          // FH_EP_PROGRAM
@@ -34,11 +36,21 @@ __device__ inline void store_out(void* y, int bf16, int64_t at, float v) {
   else ((float*)y)[at] = v;
 }
 
-// A key or value pair into the cache: x0 at column d of cache row `row` (rows counted over all 2 kv_heads planes),
-// x1 at d + head_dim / 2. A block-float cache rounds bf16(x) (nearest even) run by run as fh_bfp_pack does
-// (ferrite/compiler.py:1638-1714, put_kernel): the 16 lanes lane & ~15 .. (lane & ~15) + 15 hold a run's 16 columns,
-// in order (j = lane & 15), and all of them must be here; the run's exponent is their largest.
-__device__ inline void cache_put(const MatArgs& a, int64_t row, int d, int d1, int j, float x0, float x1) {
+// A row's place as an index into the RoPE tables: a place outside them reads their nearest row (the host checks
+// places; this keeps a bad one from reading past the tables)
+__device__ inline int64_t rope_place(const MatArgs& a, int32_t place) {
+  return place < 0 ? 0 : (place >= a.rope_rows ? a.rope_rows - 1 : place);
+}
+
+// A key or value pair into the cache: x0 at column d of row `crow` of plane ch (0 .. 2 kv_heads - 1: keys' heads
+// then values'), x1 at d + head_dim / 2. A row outside 0 .. cache_len - 1 is not written (the host checks the rows;
+// this keeps a bad one from writing past the cache). A block-float cache rounds bf16(x) (nearest even) run by run as
+// fh_bfp_pack does (ferrite/compiler.py:1638-1714, put_kernel): the 16 lanes lane & ~15 .. (lane & ~15) + 15 hold a
+// run's 16 columns, in order (j = lane & 15), and all of them must be here (they share the row, so they skip
+// together); the run's exponent is their largest.
+__device__ inline void cache_put(const MatArgs& a, int ch, int32_t crow, int d, int d1, int j, float x0, float x1) {
+  if (crow < 0 || crow >= a.cache_len) return;
+  const int64_t row = (int64_t)ch * a.cache_len + crow;
   const int hd = a.head_dim;
   if (a.cache_fmt == FH_F32 || a.cache_fmt == FH_BF16) {
     store_out(a.cache, a.cache_fmt == FH_BF16, row * hd + d, x0);
@@ -131,11 +143,12 @@ inline int epilogue_args(const char* who, const fh_epilogue* ep, int64_t K, int6
           return bad(FH_EINVAL, "FH_EP_ROPE_KV needs N = (heads + 2 kv_heads) * head_dim, head_dim a multiple of 32");
         if (!ep->cos_tab || !ep->sin_tab || !ep->places || !ep->cache_rows || !ep->cache || ep->cache_len < 1)
           return bad(FH_EINVAL, "FH_EP_ROPE_KV needs tables, places, cache rows and a cache");
+        if (ep->rope_rows < 1) return bad(FH_EINVAL, "FH_EP_ROPE_KV needs rope_rows, the rows of cos_tab and sin_tab");
         if (ep->cache_dtype < FH_F32 || ep->cache_dtype > FH_BFP4) return bad(FH_EUNSUP, "cache is FH_F32, FH_BF16, FH_BFP8 or FH_BFP4");
         if (y_dtype != FH_F32) return bad(FH_EUNSUP, "FH_EP_ROPE_KV writes q in fp32");
         a.P = 2; a.pair_half = hd / 32; out_cols = (int64_t)ep->heads * hd;
         a.heads = ep->heads; a.kv_heads = ep->kv_heads; a.head_dim = hd;
-        a.cos_tab = ep->cos_tab; a.sin_tab = ep->sin_tab; a.places = ep->places; a.cache_rows = ep->cache_rows;
+        a.cos_tab = ep->cos_tab; a.sin_tab = ep->sin_tab; a.rope_rows = ep->rope_rows; a.places = ep->places; a.cache_rows = ep->cache_rows;
         a.cache = ep->cache; a.cache_fmt = ep->cache_dtype; a.cache_len = ep->cache_len;
         a.cache_exps = (uint8_t*)ep->cache + kv_exps_at(ep->cache_dtype, ep->kv_heads, ep->cache_len, hd);
         break;

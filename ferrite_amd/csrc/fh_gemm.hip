@@ -295,7 +295,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
         const int hd = a.head_dim;
         const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
         if (h < a.heads + a.kv_heads) {  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
-          const int64_t place = a.places[m];
+          const int64_t place = rope_place(a, a.places[m]);
           const float* cs = a.cos_tab + place * hd;
           const float* sn = a.sin_tab + place * hd;
           const float t0 = x0 * cs[d] - x1 * sn[d], t1 = x1 * cs[d1] + x0 * sn[d1];
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
           q[d] = x0; q[d1] = x1;
         } else {
           const int ch = h - a.heads;
-          cache_put(a, (int64_t)ch * a.cache_len + a.cache_rows[m], d, d1, j, x0, x1);
+          cache_put(a, ch, a.cache_rows[m], d, d1, j, x0, x1);
         }
       }
     }

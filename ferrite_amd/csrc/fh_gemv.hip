@@ -62,7 +62,7 @@ __global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(MatArgs a) {
         const int at = lane + 64 * i;
         ssq_pre[b][i] = (a.ssq_in && a.ssq_parts <= 64 * PRE && at < a.ssq_parts) ? a.ssq_in[(int64_t)b * a.ssq_parts + at] : 0.f;
       }
-      place_pre[b] = a.places ? a.places[b] : 0;
+      place_pre[b] = a.places ? (int)rope_place(a, a.places[b]) : 0;
     }
   }
 
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(MatArgs a) {
       const int64_t col = nb[p] * 16 + j, at = b * a.ldy + col;
       float v = fin[i] * rs[b];
       if (kind == FH_EP_RESIDUAL) v += a.residual[at];
-      if (kind == FH_EP_PROGRAM) v = prog_eval(a.prog, v, 0, b, col);
+      if (kind == FH_EP_PROGRAM) v = prog_eval(a.prog, v, 0, a.row_base + b, col);
       store_out(a.y, a.y_bf16, at, v);
       if (kind == FH_EP_RESIDUAL && a.copy_bf16) a.copy_bf16[b * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(MatArgs a) {
         q[d] = x0; q[d1] = x1;
       } else {  // keys' heads then values' heads, each at the row's cache row
         const int ch = h - a.heads;  // 0 .. 2 kv_heads - 1
-        cache_put(a, (int64_t)ch * a.cache_len + a.cache_rows[b], d, d1, j, x0, x1);
+        cache_put(a, ch, a.cache_rows[b], d, d1, j, x0, x1);
       }
     }
   }
@@ -291,6 +291,7 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
   for (int b0 = 0; b0 < batch; b0 += p.most) {  // more rows than a launch takes: several launches, each reading W again
     const int n = batch - b0 < p.most ? batch - b0 : p.most;
     MatArgs c = a;
+    c.row_base = b0;
     c.x = (const char*)x + (size_t)b0 * ldx * 4;
     c.y = (char*)y + (size_t)b0 * ldy * (a.y_bf16 ? 2 : 4);
     if (c.ssq_in) c.ssq_in += (int64_t)b0 * c.ssq_parts;

@@ -274,7 +274,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       const int64_t at = (yrow0 + row) * a.ldy + col + col_off;
       float v = fin[row * PLD + c] * scale_s[row];
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
-      if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, row, col);
+      if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, a.row_base + row, col);
       if (ok) store_out(a.y, a.y_bf16, at, v);
       if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) a.copy_bf16[(yrow0 + row) * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
         const int hd = a.head_dim;
         const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
         if (h < a.heads + a.kv_heads) {  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
-          const int64_t place = a.places[row];
+          const int64_t place = rope_place(a, a.places[row]);
           const float* cs = a.cos_tab + place * hd;
           const float* sn = a.sin_tab + place * hd;
           const float t0 = x0 * cs[d] - x1 * sn[d], t1 = x1 * cs[d1] + x0 * sn[d1];
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
           q[d] = x0; q[d1] = x1;
         } else {
           const int ch = h - a.heads;
-          cache_put(a, (int64_t)ch * a.cache_len + a.cache_rows[row], d, d1, j, x0, x1);
+          cache_put(a, ch, a.cache_rows[row], d, d1, j, x0, x1);
         }
       }
     }
@@ -398,6 +398,7 @@ int skinny_matmul(const MatArgs& a0, const SkinnyMoe& moe, int fmt, int experts,
   }
   for (int64_t m0 = 0; m0 < a0.M; m0 += 64) {
     MatArgs a = a0;
+    a.row_base = m0;
     a.M = a0.M - m0 < 64 ? a0.M - m0 : 64;
     a.rows = rows;
     a.x = (const char*)a0.x + m0 * a0.ldx * (a0.x_bf16 ? 2 : 4);

@@ -37,7 +37,8 @@ class Epilogue(ctypes.Structure):
   _fields_ = [("kind", I), ("norm_w", P), ("ssq_in", P), ("eps", ctypes.c_float), ("centered", I),
               ("residual", P), ("ssq_out", P), ("split", I), ("heads", I), ("kv_heads", I), ("head_dim", I),
               ("cos_tab", P), ("sin_tab", P), ("places", P), ("cache_rows", P), ("cache", P), ("cache_dtype", I),
-              ("cache_len", L), ("argmax_parts", P), ("program", ctypes.POINTER(Program)), ("copy_bf16", P), ("copy_w", P)]
+              ("cache_len", L), ("argmax_parts", P), ("program", ctypes.POINTER(Program)), ("copy_bf16", P), ("copy_w", P),
+              ("rope_rows", L)]
 
 
 SIGNATURES = {

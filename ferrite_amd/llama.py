@@ -159,6 +159,7 @@ class Decoder:
     self.parts = torch.zeros(B, c.vocab // 16, dtype=torch.int64, device=self.device)  # each run of 16 logits' best
     self.ws = ops.attention_workspace(B, c.heads, hd, context, self.device)
     self.graph = None
+    self.top = 0  # the largest place of the rows set (set_rows), which advance raises
 
   def weight_bytes(self):
     """Bytes of the weights one decode step reads: every matrix, a row of the embedding, the norms."""
@@ -169,7 +170,10 @@ class Decoder:
     """Each row's place, and the cache rows: slot s's sequence keeps rows s * context .. (models/llama.py:429-452)."""
     places = torch.as_tensor(places, dtype=torch.int32)
     slots = torch.zeros_like(places) if slots is None else torch.as_tensor(slots, dtype=torch.int32)
+    if places.shape != (self.batch,) or slots.shape != (self.batch,): raise ValueError(f"set_rows: {self.batch} places and slots")
     if (places < 0).any() or (places >= min(self.context, self.c.places)).any(): raise ValueError("a place past the cache or RoPE's tables")
+    if (slots < 0).any() or (slots >= self.slots).any(): raise ValueError(f"a slot outside 0..{self.slots - 1}")
+    self.top = int(places.max())  # (the largest place, kept on the host for advance's check)
     self.places.copy_(places)
     self.first.copy_(slots * self.part)
     self.rows.copy_(slots * self.part + places)
@@ -184,7 +188,7 @@ class Decoder:
     ops.embed_rows(self.embed, self.ids, self.x, self.ssq)
     for l, L in enumerate(self.layers):
       ep = ops.epilogue(lib.EP_ROPE_KV, norm_w=L.norm1, ssq_in=self.ssq, eps=c.eps, centered=int(c.centered),
-                        heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
+                        heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin, rope_rows=self.cos.shape[0],
                         places=self.places, cache_rows=self.rows, **self._cache(l))
       ops.gemv(self.x, L.qkv, ep, out=self.q)
       ops.attention_decode(self.q, self.cache[l], c.heads, c.kv, hd, self.places, self.first, self.context, self.ws, o=self.att)
@@ -217,7 +221,7 @@ class Decoder:
     ops.embed_rows(self.embed, self.ids, self.x, self.ssq)
     rs = dict(ssq_in=self.ssq, eps=c.eps)  # rows that hold x w: 1/rms only
     for l, L in enumerate(self.layers):
-      rope = dict(heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin, places=self.places,
+      rope = dict(heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin, rope_rows=self.cos.shape[0], places=self.places,
                   cache_rows=self.rows, **self._cache(l))
       if l == 0:
         ops.rms_rows(self.x, L.norm1, c.eps, c.centered, out=self.xn)
@@ -252,6 +256,7 @@ class Decoder:
     ids = [int(i) for i in ids]
     T = len(ids)
     if T < 1 or p0 < 0 or p0 + T > min(self.context, self.c.places): raise ValueError("prefill: the prompt's places past the cache or RoPE's tables")
+    if not 0 <= slot < self.slots: raise ValueError(f"prefill: slot {slot} outside 0..{self.slots - 1}")
     chunk = chunk or T
     for a in range(0, T, chunk):
       out = self._prefill_chunk(ids[a:a + chunk], slot, p0 + a)
@@ -271,7 +276,7 @@ class Decoder:
     # more than fh_rms_rows; the batched decode takes the residual epilogues' scaled copies instead)
     for l, L in enumerate(self.layers):
       ops.rms_rows(x, L.norm1, c.eps, c.centered, out=xn)
-      ep = ops.epilogue(lib.EP_ROPE_KV, heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin,
+      ep = ops.epilogue(lib.EP_ROPE_KV, heads=c.heads, kv_heads=c.kv, head_dim=hd, cos_tab=self.cos, sin_tab=self.sin, rope_rows=self.cos.shape[0],
                         places=places, cache_rows=rows, **self._cache(l))
       ops.gemm(xn, L.qkv, ep, out=q)
       ops.attention_prefill(q, self.cache[l], c.heads, c.kv, hd, p0, slot * self.part, o=att)
@@ -303,7 +308,11 @@ class Decoder:
     return self.logits, self.picks
 
   def advance(self):
-    """Each row's next place and its pick as the next token, on the GPU (no host round trip): greedy decoding."""
+    """Each row's next place and its pick as the next token, on the GPU (no host round trip): greedy decoding. Raises
+    once a row's next place would pass the cache or RoPE's tables (the host keeps the largest place: set_rows', plus
+    one a call)."""
+    if self.top + 1 >= min(self.context, self.c.places): raise ValueError(f"advance: place {self.top + 1} past the cache or RoPE's tables")
+    self.top += 1
     self.ids.copy_(self.picks)
     self.places.add_(1)
     self.rows.add_(1)

@@ -192,8 +192,9 @@ def cache_fields(cache):
 
 
 def attention_workspace(batch, heads, head_dim, max_context, device="cuda"):
+  """fh_attention_decode's workspace, uninitialised (a workspace needs no clearing)."""
   n = lib.load().fh_attention_workspace_bytes(batch, heads, head_dim, max_context)
-  return torch.zeros(max(n, 256), dtype=torch.uint8, device=device)
+  return torch.empty(max(n, 256), dtype=torch.uint8, device=device)
 
 
 def attention_decode(q, cache, heads, kv_heads, head_dim, places, first_row, max_context, workspace, o=None):

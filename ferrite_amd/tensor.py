@@ -15,7 +15,7 @@ the tree under the root into as few launches as its shape allows, as ferrite's r
     the heaviest shared part first.
 Programs compute in fp32 and round once, to the result's dtype (bf16 to nearest even); ferrite's SFPU rounds where its
 Dst does. int32 goes through fp32, exact below 2^24, as ferrite's does for what int32 does not do itself."""
-import ctypes, math
+import collections, contextlib, ctypes, math, time
 import numpy as np
 import torch
 from ferrite_amd import lib, ops
@@ -33,23 +33,74 @@ REDUCE = {f"{f}{ax}": (f, ax) for f in ("sum", "max") for ax in range(3)}
 
 class Runtime:
   """The GPU in the place of ferrite's Runtime(chip) (ferrite/runtime.py:304-310): a device and the HIP stream every
-  launch of this runtime's tensors goes on, in order; wait() waits for them (Runtime.wait)."""
+  launch of this runtime's tensors goes on, in order. Every buffer its tensors own is allocated with that stream
+  current (on()), so torch's caching allocator hands a freed block only to later work on the same stream: a kernel
+  still queued never sees its memory reused under it. wait() waits for the launches (Runtime.wait), profile() times
+  them by name (Runtime.profile)."""
+
+  TIMES = 4096  # launches whose times profile() keeps (ferrite/runtime.py's TIMES ring)
 
   def __init__(self, device=0):
     lib.load()
     self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
     self.stream = torch.cuda.Stream(device=self.device) if self.device.type == "cuda" else None
     self.launches = 0  # kernels launched (how many a realize took)
+    self.queued = collections.deque()  # (launch, name, end event) of the launches that may not be done
+    self.times = {}  # launch % TIMES -> (launch, name, start event, end event)
 
-  def wait(self):
-    if self.stream is not None: self.stream.synchronize()
+  def on(self):
+    """A context with this runtime's stream current: torch allocations and copies inside it are ordered with its
+    launches."""
+    return torch.cuda.stream(self.stream) if self.stream is not None else contextlib.nullcontext()
 
-  def run(self, fn):
-    """fn() with this runtime's stream current (its library calls go on it)."""
+  def run(self, fn, name="launch"):
+    """fn() with this runtime's stream current (its library calls go on it), as launch number self.launches + 1 named
+    `name`; outside a graph capture it is bracketed by events, which wait() polls and profile() reads."""
     self.launches += 1
     if self.stream is None: return fn()
     with torch.cuda.stream(self.stream):
-      return fn()
+      if torch.cuda.is_current_stream_capturing(): return fn()  # (a recording's launches carry no events)
+      start = torch.cuda.Event(enable_timing=True)
+      start.record(self.stream)
+      out = fn()
+      end = torch.cuda.Event(enable_timing=True)
+      end.record(self.stream)
+    self.times[self.launches % self.TIMES] = (self.launches, name, start, end)
+    self.queued.append((self.launches, name, end))
+    return out
+
+  def wait(self, timeout=60):
+    """Until every launch queued has finished (Runtime.wait, ferrite/runtime.py:473-484): polls each launch's end
+    event, so long as launches keep finishing. None finishing in `timeout` seconds means the GPU hangs: TimeoutError,
+    naming the launch it is on and how many wait behind it."""
+    since, last = time.monotonic(), None
+    while True:
+      while self.queued and self.queued[0][2].query(): self.queued.popleft()
+      if not self.queued and (self.stream is None or self.stream.query()): return
+      head = self.queued[0][0] if self.queued else None
+      if head != last: since, last = time.monotonic(), head  # progress: the deadline starts again
+      elif time.monotonic() - since > timeout:
+        n, name, _ = self.queued[0] if self.queued else (self.launches, "a recording's launches", None)
+        raise TimeoutError(f"no launch finished in {timeout} s: the GPU is on launch {n} ({name}), "
+                           f"{max(0, len(self.queued) - 1)} queued behind it")
+      time.sleep(0.0002)
+
+  def profile(self, since):
+    """The launches after launch number `since` by name, once they are done: [(name, launches, microseconds, None)],
+    the most time first (Runtime.profile, ferrite/runtime.py:416-428). A launch's time runs between events recorded on
+    the stream before and after it; bytes read are not counted here (None). Only the last TIMES launches are kept, and
+    those replayed from a recording carry no events."""
+    self.wait()
+    assert self.launches - since <= self.TIMES, f"{self.launches - since} launches to profile, the last {self.TIMES} kept"
+    totals = {}
+    for n in range(since + 1, self.launches + 1):
+      rec = self.times.get(n % self.TIMES)
+      if rec is None or rec[0] != n: continue
+      _, name, start, end = rec
+      t = totals.setdefault(name, [0, 0.0])
+      t[0] += 1
+      t[1] += start.elapsed_time(end) * 1000.0
+    return sorted(((name, k, us, None) for name, (k, us) in totals.items()), key=lambda r: -r[2])
 
 
 class Tensor:
@@ -80,7 +131,8 @@ class Tensor:
     assert dtype not in BFP, "a block float is made on the GPU, by cast"
     matrices = data if isinstance(data[0][0], (list, tuple)) else [data]
     a = torch.tensor(matrices, dtype=torch.int32 if dtype == "int32" else torch.float32)
-    return cls._stored(rt, a.to(TORCH[dtype]).to(rt.device), dtype)
+    with rt.on():  # (its memory allocated and filled on the runtime's stream)
+      return cls._stored(rt, a.to(TORCH[dtype]).to(rt.device), dtype)
 
   @classmethod
   def frombytes(cls, rt, rows, cols, data, batch=1, dtype="bf16"):
@@ -89,14 +141,15 @@ class Tensor:
     n = ITEMSIZE[dtype]
     assert len(data) == n * batch * rows * cols, f"{len(data)} bytes for {batch} x {rows} x {cols} of {dtype}"
     raw = torch.frombuffer(bytearray(data), dtype={2: torch.int16, 4: torch.int32}[n]).reshape(batch, rows, cols)
-    return cls._stored(rt, raw.view(TORCH[dtype]).to(rt.device), dtype)
+    with rt.on():
+      return cls._stored(rt, raw.view(TORCH[dtype]).to(rt.device), dtype)
 
   def tobytes(self):
     """dtype's values in row-major order, as frombytes takes them (a block float's as bf16: each of its values is one,
     tensor._bf16s's). Waits for the launches queued."""
     x = self.realize()
     if x.dtype in BFP:
-      t = x.rt.run(lambda: torch.stack([ops.dequant(w) for w in _matrices(x)]))
+      t = x.rt.run(lambda: torch.stack([ops.dequant(w) for w in _matrices(x)]), "dequant")
     else:
       if not x.data.is_contiguous(): x = (x + 0).realize()  # a view: copied by our kernel first
       t = x.data
@@ -183,12 +236,12 @@ class Tensor:
       x = self.realize()
       if x.dtype == "int32" or not x.data.is_contiguous(): x = (x.float() if x.dtype == "int32" else x + 0).realize()
       out = Tensor(self.rt, self.rows, self.cols, batch=x.batch, dtype=dtype)
-      packed = [x.rt.run(lambda b=b: ops.pack(x.data[b], dtype)) for b in range(x.batch)]
+      packed = [x.rt.run(lambda b=b: ops.pack(x.data[b], dtype), "pack") for b in range(x.batch)]
       out.data = packed[0] if x.batch == 1 else packed
       return out
     if self.dtype in BFP:  # a block float's values (each a bf16 value)
       b = Tensor(self.rt, self.rows, self.cols, batch=self.batch, dtype="bf16")
-      b.data = self.rt.run(lambda: torch.stack([ops.dequant(w) for w in _matrices(self)]))
+      b.data = self.rt.run(lambda: torch.stack([ops.dequant(w) for w in _matrices(self)]), "dequant")
       return b.cast(dtype)
     return Tensor(self.rt, self.rows, self.cols, "cast", (self,), self.batch, dtype)
 
@@ -266,11 +319,11 @@ class Tensor:
     assert self.dtype in ("bf16", "fp32") and 1 <= k <= min(self.cols, 64), "bf16 or fp32, k of at most 64"
     n, cols = self.batch * self.rows, self.cols
     ld = (cols + 3) // 4 * 4  # rows 16-byte aligned for the kernel's loads
-    x = torch.empty(n, ld, dtype=torch.float32, device=self.rt.device)
+    with self.rt.on(): x = torch.empty(n, ld, dtype=torch.float32, device=self.rt.device)
     prog, inputs = _fit_program(self.float() if self.dtype != "fp32" else self, self.shape, allow_acc=False)
     p = _cprogram(prog, inputs)
-    self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(x), lib.F32, *self.shape, self.rows * ld, ld, ops._stream()))
-    values, ids = self.rt.run(lambda: ops.logit_heads(x[:, :cols], k))
+    self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(x), lib.F32, *self.shape, self.rows * ld, ld, ops._stream()), "map")
+    values, ids = self.rt.run(lambda: ops.logit_heads(x[:, :cols], k), "topk")
     v = Tensor(self.rt, self.rows, k, batch=self.batch, dtype="fp32")
     v.data = values.reshape(self.batch, self.rows, k)
     i = Tensor(self.rt, self.rows, k, batch=self.batch, dtype="int32")
@@ -311,7 +364,7 @@ class Tensor:
       prog, inputs = _fit_program(self, self.shape, allow_acc=False)  # (a stored tensor: one copy op)
       p = _cprogram(prog, inputs)
       out, ld = into.data, into.data.stride()
-      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[into.dtype], *into.shape, ld[0], ld[1], ops._stream()))
+      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[into.dtype], *into.shape, ld[0], ld[1], ops._stream()), "map")
       return into
     if self.data is not None: return self
     if self.op == "picked":
@@ -321,15 +374,15 @@ class Tensor:
       f, axis = REDUCE[self.op]
       src = self.srcs[0]
       prog, inputs = _fit_program(src, src.shape, allow_acc=False)
-      out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
+      with self.rt.on(): out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
       p = _cprogram(prog, inputs)
       self.rt.run(lambda: lib.call("fh_reduce", ctypes.byref(p), lib.REDUCE_MAX if f == "max" else lib.REDUCE_SUM, axis,
-                                   *src.shape, ops._ptr(out), DT[self.dtype], ops._stream()))
+                                   *src.shape, ops._ptr(out), DT[self.dtype], ops._stream()), "reduce")
       self._done(out)
       return self
     prog, inputs = _fit_program(self, self.shape, allow_acc=True)
     mm = next((t for t in _walk(self) if getattr(t, "_acc", False)), None)
-    out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
+    with self.rt.on(): out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
     p = _cprogram(prog, inputs)
     if mm is not None:
       mm._acc = False
@@ -343,12 +396,12 @@ class Tensor:
       ep.keep.append(program)
       if w.K % 32 or (a.dtype == "fp32" and a.rows <= 8):  # fp32 rows, or a K the matrix cores do not take: the
         if x.dtype != torch.float32: x = a.float().realize().data[0]  # exact-product GEMV
-        self.rt.run(lambda: ops.gemv(x, w, ep, out=y))
+        self.rt.run(lambda: ops.gemv(x, w, ep, out=y), "matmul")
       else:  # the matrix cores (bf16 rows go in as they are: their products are exact too)
-        self.rt.run(lambda: ops.gemm(x, w, ep, out=y))
+        self.rt.run(lambda: ops.gemm(x, w, ep, out=y), "matmul")
     else:
       ld = out.stride()
-      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[self.dtype], *self.shape, ld[0], ld[1], ops._stream()))
+      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[self.dtype], *self.shape, ld[0], ld[1], ops._stream()), "map")
     self._done(out)
     return self
 

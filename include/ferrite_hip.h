@@ -4,9 +4,10 @@
  * Every entry point takes plain device pointers and sizes, enqueues its kernels on `stream` (a hipStream_t, NULL for the
  * default stream) and returns at once: 0 on success, a negative FH_E* code otherwise, with the reason in
  * fh_last_error() (thread-local). Nothing here allocates or frees device memory: the caller owns every buffer, and
- * scratch comes in through a `workspace` argument sized by the matching *_workspace_bytes call, zero-filled once by
- * the caller when it is allocated (the kernels leave it zeroed after every call). Calls on one stream run in order;
- * calls that share a workspace must not overlap.
+ * scratch comes in through a `workspace` argument sized by the matching *_workspace_bytes call. A workspace needs no
+ * clearing, ever: no call keeps state in it, and what a call reads there it wrote first in the same call (a freshly
+ * allocated, uninitialised buffer is fine). Calls on one stream run in order; calls that share a workspace must not
+ * overlap.
  *
  * The reference (alkinun/ferrite) has no C interface for this path: it builds Tensix kernels in Python
  * (ferrite/compiler.py) and launches them through ferrite/runtime.py. Each declaration below names the reference
@@ -144,6 +145,10 @@ typedef struct fh_epilogue {
    * (bf16(x * w), then 1/rms on the sums). */
   void* copy_bf16;
   const float* copy_w;
+  /* FH_EP_ROPE_KV: the rows of cos_tab and sin_tab (the places they cover). A place outside 0 .. rope_rows - 1 reads
+   * the nearest row, and a cache row outside 0 .. cache_len - 1 is not written: the caller checks both, these keep a
+   * bad value from reading or writing past the buffers. */
+  int64_t rope_rows;
 } fh_epilogue;
 
 /* y (dtype y_dtype, row stride ldy) from x @ W and the epilogue. x: fp32. w_mant/w_exps: a packed [K][N] weight

@@ -5,8 +5,9 @@ package, and only to check or to time the CPU path; the product (ferrite_amd) ne
 
 Each function cites the reference file:line it follows (paths under alkinun/ferrite). How each is pinned, beyond
 restating it: tests/test_oracle.py checks bf16_bits against exact rational rounding, bfp against an independent
-rational-arithmetic rounding of every (bf16 value, block exponent) pair, decode_bf16 against q * 2^(e - 133) over
-every (q, e, sign), and all of them against the golden vectors in tests/golden written from the reference itself.
+rational-arithmetic rounding of every (bf16 value, block exponent) pair, and decode_bf16 against q * 2^(e - 133) over
+every (q, e, sign). The reference commits no golden vectors for these functions and cannot be imported here, so no
+vectors were written from it.
 """
 import numpy as np
 

@@ -20,7 +20,7 @@ import numpy as np
 from oracle.bfp import bf16, bf16_bits, bf16_floats, bfp
 
 DEFAULTS = dict(head_dim=None, rope=None, k=0, experts=0, norm_topk=True, centered=False, tied=False, precision=None,
-                places=4096, vocab=0, ffn=0)
+                places=4096, vocab=0, ffn=0, mtp=0)
 
 
 def model(**c):
@@ -33,9 +33,12 @@ def head(c):  # llama.py:87
 
 
 def precision(c, mode="bf16", kv=None):
-  """Each matmul's weights' (format, phases) (models/llama.py:54-76), the modes on this path: bf16, bfp8, bfp4 (the
-  MLP's gate and up in bfp4), experts (every MLP matrix in bfp4). Phases are the chip's alone: the GPU's products are
-  exact at any."""
+  """Each matmul's weights' (format, phases) (models/llama.py:54-76): bf16, bfp8, bfp4 (the MLP's gate and up in
+  bfp4), tt (bfp4's formats at one phase for a bfp4 B and two for a bfp8 one; Llama-3.1-8B's last gate_up in bfp8),
+  experts (every MLP matrix in bfp4 at one phase, the rest bfp8 at two, and a draft head of the output layer in bfp4).
+  The key ("kv", None) is the KV cache's format (tt's and experts' bfp8, else bf16). Phases are the chip's alone: the
+  GPU's products are exact at any. Pinned by the reference's own answers (test_sim.py:1999-2008) in
+  tests/test_precision.py."""
   four = {"bfp4": ("gate_up",), "tt": ("gate_up",), "experts": ("gate_up", "down")}.get(mode, ())
   fast = mode in ("tt", "experts")
 
@@ -43,9 +46,10 @@ def precision(c, mode="bf16", kv=None):
     if mode in ("bf16", "bfp8"): return mode, 4
     f = "bfp4" if op in four else "bfp8"
     return f, ((1 if f == "bfp4" else 2) if fast else 4)
-  p = {(op, l): entry(op) for l in range(c.layers) for op in ("qkv", "o", "gate_up", "down")}
+  p = {(op, l): entry(op) for l in range(c.layers + c.mtp) for op in ("qkv", "o", "gate_up", "down")}
   if mode == "tt" and (c.layers, c.dim) == (32, 4096): p["gate_up", 31] = ("bfp8", 2)
   p["head", None] = entry("head")
+  if mode == "experts": p["draft head", None] = ("bfp4", 1)
   attention = {("attention", "decode"): (None, 2 if mode == "tt" else 4), ("attention", "prefill"): (None, 4)}
   return p | attention | {("kv", None): (kv or ("bfp8" if fast else "bf16"), None)}
 
@@ -54,7 +58,7 @@ def weight_format(name, prec):
   """A weight's format (models/llama.py:615-623): the matrices a matmul reads as its B in prec's, the rest bf16."""
   op = name.split(".")[-1].removesuffix("_proj")
   matrix = name.endswith(("_proj", "experts.gate_up", "experts.down"))
-  key = {"embed.T": ("head", None)}.get(name) or ((op, int(name.split(".")[1])) if matrix else None)
+  key = {"embed.T": ("head", None), "embed.T draft": ("draft head", None)}.get(name) or ((op, int(name.split(".")[1])) if matrix else None)
   return prec[key][0] if prec and key in prec else "bf16"
 
 
@@ -214,6 +218,40 @@ def forward(ids, places, w, c, caches, every=False):
     x = layer(x, block(w, f"layers.{l}."), c, (cos, sin, t), mask, caches[l], places)
   h = rms(x, w["norm"], c)
   return (h if every else h[-1:]) @ w["embed.T"]
+
+
+def forward_slots(ids, places, w, c, caches):
+  """Several sequences decoding together, one token each (models/llama.py:459-480 with slots, attention's slots branch
+  at 133-137 and around's rows, 429-452): the matmuls take every row at once, each row's keys and values go to its own
+  sequence's cache (caches[b], one kv_cache of its own rather than a part of a shared one: the same rows) at its place,
+  and it attends over that sequence's places up to its own. Every row's logits. (The reference's convention for a free
+  slot, a token on its part's last row seeing only the part's first, serves idle slots of a server and is not
+  restated: every row here is live.)"""
+  x = w["embed"][list(ids)]
+  places = np.asarray(places)
+  cos, sin, t = w["cos"][places], w["sin"][places], w["turn"]
+  size = caches[0][0].shape[-2]
+  hd, rep, nh = head(c), c.heads // c.kv, c.heads + 2 * c.kv
+  for l in range(c.layers):
+    p = block(w, f"layers.{l}.")
+    h = rms(x, p["input_layernorm"], c)
+    qkv = merge(rope(split(h @ p["qkv_proj"], nh), split(cos, nh), split(sin, nh), t))
+    heads = split(qkv, nh)  # [heads][rows][hd]
+    fmt = (c.precision or {}).get(("kv", None), ("bf16", None))[0]
+    o = np.zeros((len(ids), c.heads * hd))
+    for b, place in enumerate(places):
+      kv = heads[c.heads:, b:b + 1]
+      if fmt in ("bfp8", "bfp4"): kv = bfp(kv, fmt)
+      elif fmt == "bf16" and getattr(c, "kv_rounded", False): kv = bf16(kv)
+      cache = caches[b][l]
+      cache[:, [place]] = kv
+      k, v = np.repeat(cache[:c.kv], rep, 0), np.repeat(cache[c.kv:], rep, 0)
+      s = (heads[:c.heads, b:b + 1] @ k.swapaxes(-1, -2)) * (1 / math.sqrt(hd)) + masked([place], size)
+      o[b] = merge(softmax(s) @ v)[0]
+    x = x + o @ p["o_proj"]
+    h = rms(x, p["post_attention_layernorm"], c)
+    x = x + (moe(h, p, c)[0] if "router" in p else mlp(h, p))
+  return rms(x, w["norm"], c) @ w["embed.T"]
 
 
 def prefill(ids, w, c, caches, tokens):  # llama.py:498-504: a prompt so many tokens at a time

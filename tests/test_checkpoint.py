@@ -42,3 +42,26 @@ def test_refuses_what_it_cannot_read(tmp_path):
   (tmp_path / "config.json").write_text(json.dumps(cfg))
   with pytest.raises(NotImplementedError, match="yarn"):
     K.config(str(tmp_path))
+
+
+@pytest.mark.parametrize("extra,match", [({"sliding_window": 64}, "sliding window"), ({"layer_types": ["linear_attention"]}, "layer_types"),
+                                         ({"model_type": "qwen3_5_moe"}, "qwen3_5"), ({"shared_expert_intermediate_size": 32}, "shared_expert")])
+def test_refuses_blocks_it_cannot_run(tmp_path, extra, match):
+  # a config whose blocks this path does not run raises rather than loading into wrong logits; a window that covers
+  # every place the tables hold changes nothing and loads
+  cfg = {"hidden_size": 16, "num_attention_heads": 1, "num_key_value_heads": 1, "num_hidden_layers": 1, "rms_norm_eps": 1e-5,
+         "rope_theta": 1e4, "max_position_embeddings": 256, "vocab_size": 4, "intermediate_size": 16}
+  (tmp_path / "config.json").write_text(json.dumps(cfg | extra))
+  with pytest.raises(NotImplementedError, match=match):
+    K.config(str(tmp_path), places=128)
+  (tmp_path / "config.json").write_text(json.dumps(cfg | {"sliding_window": 4096}))
+  assert K.config(str(tmp_path), places=128).places == 128
+
+
+@pytest.mark.parametrize("name", ["model.layers.0.self_attn.q_proj.bias", "model.layers.0.self_attn.k_norm.weight"])
+def test_refuses_tensors_it_cannot_apply(tmp_path, name):
+  # Qwen2's q/k/v biases and Qwen3's q/k norms are refused at load, not silently dropped
+  C.write_safetensors(tmp_path / "model.safetensors", {"model.embed_tokens.weight": np.zeros((4, 16), np.float32),
+                                                       name: np.zeros((16,), np.float32)})
+  with pytest.raises(NotImplementedError, match="not on this path"):
+    K.Checkpoint(str(tmp_path), device="cpu")

@@ -178,7 +178,7 @@ def test_epilogues(cuda):
       cache = torch.zeros(2 * c.kv, 64, hd, dtype=cache_dtype, device="cuda")
       cos, sin = OL.rotary_head(c, c.places)
       ep = ops().epilogue(L.EP_ROPE_KV, norm_w=to_gpu(g.reshape(-1)), ssq_in=to_gpu(ssq), eps=c.eps, heads=c.heads,
-                          kv_heads=c.kv, head_dim=hd, cos_tab=to_gpu(cos), sin_tab=to_gpu(sin), places=to_gpu(places, torch.int32),
+                          kv_heads=c.kv, head_dim=hd, cos_tab=to_gpu(cos), sin_tab=to_gpu(sin), rope_rows=len(cos), places=to_gpu(places, torch.int32),
                           cache_rows=to_gpu(rows, torch.int32), cache=cache, cache_dtype=L.DTYPES["fp32" if cache_dtype == torch.float32 else "bf16"],
                           cache_len=64)
       q = ops().gemv(to_gpu(x), ops().pack(to_gpu(w)), ep).cpu().numpy()

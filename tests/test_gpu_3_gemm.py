@@ -156,7 +156,7 @@ def test_gemm_epilogues(cuda, M):
   for cache_dtype in (torch.float32, torch.bfloat16):
     cache = torch.zeros(2 * c.kv, c.places + 8, hd, dtype=cache_dtype, device="cuda")
     ep = ops().epilogue(L.EP_ROPE_KV, norm_w=to_gpu(g.reshape(-1)), ssq_in=to_gpu(ssq), eps=c.eps, heads=c.heads,
-                        kv_heads=c.kv, head_dim=hd, cos_tab=to_gpu(cos), sin_tab=to_gpu(sin), places=to_gpu(places, torch.int32),
+                        kv_heads=c.kv, head_dim=hd, cos_tab=to_gpu(cos), sin_tab=to_gpu(sin), rope_rows=len(cos), places=to_gpu(places, torch.int32),
                         cache_rows=to_gpu(rows, torch.int32), cache=cache,
                         cache_dtype=L.DTYPES["fp32" if cache_dtype == torch.float32 else "bf16"], cache_len=c.places + 8)
     q = ops().gemm(to_gpu(x), ops().pack(to_gpu(w)), ep).cpu().numpy()

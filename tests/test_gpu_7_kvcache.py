@@ -101,7 +101,7 @@ def test_rope_kv_puts_block_floats(cuda, path, M, hd, heads, kv):
   for fmt in ("bf16",) + FMTS:
     cache = ops().kv_cache(2 * kv, length, hd, fmt)
     data, dtype, n = ops().cache_fields(cache)
-    ep = ops().epilogue(lib().EP_ROPE_KV, heads=heads, kv_heads=kv, head_dim=hd, cos_tab=to_gpu(cos), sin_tab=to_gpu(sin),
+    ep = ops().epilogue(lib().EP_ROPE_KV, heads=heads, kv_heads=kv, head_dim=hd, cos_tab=to_gpu(cos), sin_tab=to_gpu(sin), rope_rows=len(cos),
                         places=to_gpu(places, torch.int32), cache_rows=to_gpu(rows, torch.int32), cache=data,
                         cache_dtype=dtype, cache_len=n)
     outs[fmt] = (mm(xin, bw, ep).cpu().numpy(), cache)

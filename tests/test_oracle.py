@@ -161,3 +161,27 @@ def test_head_of_pinned():
       want = sorted(range(n), key=lambda c: (-x[c], c))[:k]
       assert list(i) == want and np.array_equal(v, x[want])
       assert abs(lse - logsumexp(np.float64(x) * t)) <= 1e-12 * abs(lse) + 1e-12
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+def test_c_restatement_is_numpys(fmt):
+  # oracle/bfp_c.c (the full-width tests' bfp) against oracle/bfp.py's bfp, bit for bit: every finite bf16 value in a
+  # run with 15 others whose largest exponent is drawn from 0..254 (so every shift, subnormal scales included), as bf16
+  # bits and as float32 values, and random float32 matrices (rounded to bf16 first)
+  from oracle import cbfp
+  rng = np.random.default_rng(7)
+  allv = np.arange(65536, dtype=np.uint32)
+  allv = allv[((allv >> 7) & 255) != 255].astype(np.uint16)  # finite values
+  runs = np.empty((allv.size, 16), np.uint16)
+  runs[:, 0] = allv
+  tops = rng.integers(0, 255, allv.size)
+  for j in range(1, 16):  # exponents at most the drawn top, one of them the top itself
+    e = np.minimum(rng.integers(0, 255, allv.size), tops) if j > 1 else tops
+    runs[:, j] = (rng.integers(0, 2, allv.size) << 15 | e << 7 | rng.integers(0, 128, allv.size)).astype(np.uint16)
+  for a in (runs, O.bf16_floats(runs)):
+    got = cbfp.bfp(a, fmt)
+    want = O.bfp(O.bf16_floats(runs), fmt).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), fmt
+  m = rng.normal(0, 0.02, (64, 4096)).astype(np.float32)
+  m[3, :16] = 0
+  assert np.array_equal(cbfp.bfp(m, fmt).view(np.uint32), O.bfp(m, fmt).astype(np.float32).view(np.uint32))

@@ -127,4 +127,31 @@ def test_moe_matches_mixtral():
   with torch.no_grad():
     want = blk(t(h)[None])[0].numpy() if not isinstance(blk(t(h)[None]), tuple) else blk(t(h)[None])[0][0].numpy()
   assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max(), np.abs(got - want).max()
-  assert (np.sort(ids, 1) == np.sort(ids, 1)).all() and np.allclose(wts.sum(1), 1)
+  # the picks: the oracle's ids, largest first, are the router's top-k indices, and its weights the router's
+  # renormalised top-k probabilities (transformers' router computes them in float32)
+  with torch.no_grad():
+    _, scores, idx = blk.gate(t(h))
+  assert np.array_equal(ids, idx.numpy()), (ids, idx.numpy())
+  assert np.abs(wts - scores.numpy()).max() <= 1e-6 and np.allclose(wts.sum(1), 1)
+
+
+def test_forward_slots_is_each_sequences_forward():
+  # several sequences a step (forward_slots, models/llama.py's slots) against each sequence's own forward: the same
+  # logits, row by row, and the same caches; a slip in a row's own cache or place would differ by far more
+  rng = np.random.default_rng(24)
+  c = small()
+  w = OL.random_weights(c, rng, sd=0.05, norm_sd=0.3)
+  S, size = 3, 16
+  caches = [OL.kv_cache(c, size) for _ in range(S)]
+  alone = [OL.kv_cache(c, size) for _ in range(S)]
+  prompts = [[int(i) for i in rng.integers(0, c.vocab, n)] for n in (5, 9, 1)]
+  for b, ids in enumerate(prompts):  # the sequences' prompts, each into both of its caches
+    OL.forward(ids, range(len(ids)), w, c, caches[b])
+    OL.forward(ids, range(len(ids)), w, c, alone[b])
+  toks, places = [3, 17, 40], [len(p) for p in prompts]
+  got = OL.forward_slots(toks, places, w, c, caches)
+  for b in range(S):
+    want = OL.forward([toks[b]], [places[b]], w, c, alone[b])[0]
+    # (the first block's float32 products sum in BLAS's order for 3 rows or 1: within float32's rounding)
+    assert np.abs(got[b] - want).max() <= 1e-6 * np.abs(want).max(), b
+    assert all(np.abs(x - y).max() <= 1e-6 * np.abs(y).max() for x, y in zip(caches[b], alone[b]))
