@@ -16,6 +16,7 @@
 // run's values are bf16 values), so its results are bit for bit a bf16 cache's of those values.
 #include <math.h>
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 #include "fh_common.h"
 
@@ -542,6 +543,52 @@ extern "C" size_t fh_kv_cache_bytes(int cache_dtype, int kv_heads, int64_t cache
     case FH_BFP8: case FH_BFP4: return (size_t)(kv_exps_at(cache_dtype, kv_heads, cache_len, head_dim) + rows * (head_dim / 16));
     default: return 0;
   }
+}
+
+namespace fh {
+
+// The scratch of fh_attention_decode_noalloc: the chunks' partial results, in a fixed array the library holds on every
+// GPU it runs on (one copy a device, at its own address, until the process ends). In host code `scratch` names a
+// host-side stand-in, not device memory: host code uses only the per-device address hipGetSymbolAddress gives.
+static __device__ __align__(256) unsigned char scratch[FH_ATTENTION_SCRATCH_BYTES];
+
+// The current device's address of `scratch`, looked up once per device (with that device current) and kept.
+static int scratch_address(void** out) {
+  constexpr int MAX_DEVICES = 64;
+  static std::mutex mu;
+  static void* at[MAX_DEVICES] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(FH_EHIP, "fh_attention_decode_noalloc: no current device");
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(FH_EUNSUP, "fh_attention_decode_noalloc: device index past 63");
+  std::lock_guard<std::mutex> hold(mu);
+  if (!at[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("fh_attention_decode_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return FH_EHIP;
+    }
+    at[dev] = p;
+  }
+  *out = at[dev];
+  return FH_OK;
+}
+
+}  // namespace fh
+
+extern "C" int fh_attention_decode_noalloc(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch,
+                                           int heads, int kv_heads, int head_dim, const int32_t* places,
+                                           const int32_t* first_row, int64_t max_context, void* o, int o_dtype,
+                                           void* stream) {
+  // (the bound first, on the host: a call past it is refused before any HIP call)
+  if (batch >= 1 && heads >= 1 && head_dim >= 1 && max_context >= 1 &&
+      fh_attention_workspace_bytes(batch, heads, head_dim, max_context) > FH_ATTENTION_SCRATCH_BYTES)
+    return fail(FH_EINVAL, "fh_attention_decode_noalloc: batch x heads x context needs more scratch than "
+                           "FH_ATTENTION_SCRATCH_BYTES (16 MiB): use fh_attention_decode with a workspace");
+  void* ws = nullptr;
+  if (int rc = scratch_address(&ws)) return rc;
+  return fh_attention_decode(q, cache, cache_dtype, cache_len, batch, heads, kv_heads, head_dim, places, first_row,
+                             max_context, o, o_dtype, ws, FH_ATTENTION_SCRATCH_BYTES, stream);
 }
 
 extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch,

@@ -53,6 +53,7 @@ SIGNATURES = {
   "fh_attention_workspace_bytes": ([I, I, I, L], S),
   "fh_kv_cache_bytes": ([I, I, L, I], S),
   "fh_attention_decode": ([P, P, I, L, I, I, I, I, P, P, L, P, I, P, S, P], I),
+  "fh_attention_decode_noalloc": ([P, P, I, L, I, I, I, I, P, P, L, P, I, P], I),
   "fh_attention_prefill": ([P, L, P, I, L, I, I, I, I, L, L, P, I, L, P], I),
   "fh_rms_rows": ([P, L, L, L, P, ctypes.c_float, I, P, I, L, P], I),
   "fh_moe_route": ([P, L, I, L, P, ctypes.c_float, I, P, I, I, I, I, P, P, P, P], I),

@@ -199,6 +199,19 @@ int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int6
                         int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row, int64_t max_context,
                         void* o, int o_dtype, void* workspace, size_t ws_bytes, void* stream);
 
+/* fh_attention_decode with no workspace, for callers that cannot allocate (code under HIP graph capture, serving
+ * loops and harnesses that forbid hipMalloc); no counterpart in the reference. It allocates nothing: the chunks'
+ * partial results go to a scratch array of FH_ATTENTION_SCRATCH_BYTES (16 MiB) that the library holds on each GPU it
+ * runs on, from the first call on that GPU until the process ends. A call whose
+ * fh_attention_workspace_bytes(batch, heads, head_dim, max_context) exceeds that returns FH_EINVAL (an 8B model's 32
+ * heads at context 2048 fit up to batch 16). Every call on one GPU shares that GPU's array: calls in order on one
+ * stream are safe, calls that overlap on one GPU (several streams or threads at once) race. The array needs no
+ * clearing (no call reads what it did not write). The stream's device must be the current device. */
+#define FH_ATTENTION_SCRATCH_BYTES (16u << 20)
+int fh_attention_decode_noalloc(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch,
+                                int heads, int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row,
+                                int64_t max_context, void* o, int o_dtype, void* stream);
+
 /* A prompt's causal attention (models/llama.py:129-142 over a chunk of consecutive places; prefill, 498-504): rows
  * t = 0 .. T-1 of q [T][ldq] (fp32) are places p0 + t of the sequence whose cache rows start at slot_row; row t
  * attends to cache rows slot_row .. slot_row + p0 + t, which must already hold its keys and values (the qkv GEMM's
