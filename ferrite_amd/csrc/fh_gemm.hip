@@ -250,7 +250,17 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
   __syncthreads();
 
   const int kind = a.kind;
-  if (a.P == 1) {  // FH_EP_STORE, FH_EP_RESIDUAL, FH_EP_PROGRAM: a thread a column, 2 rows a pass; a run is 16 lanes
+  if (a.P == 1 && kind == FH_EP_PROGRAM) {  // (a loop of its own: the program's decoding, hoisted out of the loop,
+                                            // runs only here)
+    const int c = t & 127;
+    const int64_t run = tile_run(a, tn, c >> 4);
+    const int64_t col = run * 16 + (c & 15);
+    for (int r = t >> 7; r < GM_BM; r += 2) {
+      const int64_t m = m0 + r;
+      if (m < M && run >= 0)
+        store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + col, prog_eval(a.prog, Cs[r * GM_LDC + c] * rs_s[r], 0, m, col));
+    }
+  } else if (a.P == 1) {  // FH_EP_STORE, FH_EP_RESIDUAL: a thread a column, 2 rows a pass; a run is 16 lanes
     const int c = t & 127, j = c & 15;
     const int64_t run = tile_run(a, tn, c >> 4);
     const int64_t col = run * 16 + j;
@@ -260,7 +270,6 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
       const int64_t at = (ybase + m) * a.ldy + col;
       float v = Cs[r * GM_LDC + c] * rs_s[r];
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
-      if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, m, col);
       if (ok) store_out(a.y, a.y_bf16, at, v);
       if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) a.copy_bf16[m * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
@@ -293,7 +302,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
         store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + c0, silu(x0) * x1 * sc);
       } else {  // FH_EP_ROPE_KV
         const int hd = a.head_dim;
-        const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
+        const int h = (int)c0 / hd, d = (int)c0 % hd, d1 = d + hd / 2;  // (c0 < N < 2^31)
         if (h < a.heads + a.kv_heads) {  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
           const int64_t place = rope_place(a, a.places[m]);
           const float* cs = a.cos_tab + place * hd;

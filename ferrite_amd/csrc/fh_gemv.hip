@@ -147,13 +147,18 @@ __global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(MatArgs a) {
 
   // the epilogue, a lane an output (or a pair of them)
   const int kind = a.kind;
-  if (kind == FH_EP_STORE || kind == FH_EP_RESIDUAL || kind == FH_EP_PROGRAM) {
+  if (kind == FH_EP_PROGRAM) {  // (a loop of its own: the program's decoding, hoisted out of the loop, runs only here)
+    for (int i = lane; i < V; i += 64) {
+      const int b = i / (P * 16), p = (i / 16) % P, j = i % 16;
+      const int64_t col = nb[p] * 16 + j;
+      store_out(a.y, a.y_bf16, b * a.ldy + col, prog_eval(a.prog, fin[i] * rs[b], 0, a.row_base + b, col));
+    }
+  } else if (kind == FH_EP_STORE || kind == FH_EP_RESIDUAL) {
     for (int i = lane; i < V; i += 64) {  // (V is a multiple of 16: a run's 16 values are 16 neighbouring lanes)
       const int b = i / (P * 16), p = (i / 16) % P, j = i % 16;
       const int64_t col = nb[p] * 16 + j, at = b * a.ldy + col;
       float v = fin[i] * rs[b];
       if (kind == FH_EP_RESIDUAL) v += a.residual[at];
-      if (kind == FH_EP_PROGRAM) v = prog_eval(a.prog, v, 0, a.row_base + b, col);
       store_out(a.y, a.y_bf16, at, v);
       if (kind == FH_EP_RESIDUAL && a.copy_bf16) a.copy_bf16[b * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(MatArgs a) {
     for (int i = lane; i < B * 16; i += 64) {
       const int b = i / 16, j = i % 16;
       const int64_t c0 = nb[0] * 16 + j;            // in the first half of its head
-      const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
+      const int h = (int)c0 / hd, d = (int)c0 % hd, d1 = d + hd / 2;  // (c0 < N < 2^31)
       const float r = rs[b];
       float x0 = fin[(b * P) * 16 + j] * r, x1 = fin[(b * P + 1) * 16 + j] * r;
       int place = place_pre[0];

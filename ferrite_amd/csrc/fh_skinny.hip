@@ -48,7 +48,6 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   extern __shared__ __attribute__((aligned(16))) char sk_smem[];
   __shared__ float rs_s[16 * MB];
   __shared__ float scale_s[16 * MB];
-  __shared__ int any_s;
 
   const int item = blockIdx.x, e = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), W = blockDim.x >> 6;
@@ -64,17 +63,22 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   };
   const int64_t yrow0 = list0;
 
-  // the rows' weights for this expert; an expert no row picked writes its zeros and reads nothing
-  if (t == 0) any_s = gathered ? M > 0 : (moe.row_scale ? 0 : 1);
-  __syncthreads();
+  // the rows' weights for this expert (read by the epilogue, after the stream's barrier); an expert no row picked
+  // writes its zeros and reads nothing. No workgroup barrier comes before the stream: a barrier waits for every load
+  // issued before it, which would put a whole memory latency in front of the first weight loads. Each wave decides
+  // for itself whether the expert has rows.
+  bool any = true;
+  if (gathered) any = M > 0;
+  else if (moe.row_scale) {
+    const float r = lane < min(M, 16 * MB) ? moe.row_scale[(int64_t)lane * moe.experts + e] : 0.f;
+    any = __ballot(r != 0.f) != 0;
+  }
   if (t < 16 * MB) {
     float sc = 1.f;
     if (gathered) {
       if (moe.scale_rows) sc = t < M ? moe.row_w[list0 + t] : 0.f;
-    } else if (moe.row_scale) {
-      const float r = t < M ? moe.row_scale[(int64_t)t * moe.experts + e] : 0.f;
-      if (r != 0.f) any_s = 1;
-      if (moe.scale_rows) sc = r;
+    } else if (moe.row_scale && moe.scale_rows) {
+      sc = t < M ? moe.row_scale[(int64_t)t * moe.experts + e] : 0.f;
     }
     scale_s[t] = sc;
   }
@@ -91,7 +95,6 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
   float sq[SQ];
 #pragma unroll
   for (int i = 0; i < SQ; ++i) sq[i] = sqp[min(sk + tpr * i, sqn - 1)];
-  __syncthreads();
 
   // the item's two runs
   int64_t nb[2];
@@ -111,7 +114,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
 
   uint16_t* Bs = (uint16_t*)sk_smem + wave * SK_TILE;
   const int r0 = wave * a.rows, r1 = min(K, r0 + a.rows);
-  if (any_s && r0 < r1) {
+  if (any && r0 < r1) {
     const uint8_t* mrun[R];
     const uint8_t* erun[R];
 #pragma unroll
@@ -265,7 +268,16 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
 
   const int kind = a.kind;
   const int64_t col_off = (int64_t)e * moe.expert_cols;
-  if (a.P == 1) {  // FH_EP_STORE / FH_EP_RESIDUAL / FH_EP_PROGRAM: a thread a column of a row; a run is 16 lanes
+  if (a.P == 1 && kind == FH_EP_PROGRAM) {  // (a loop of its own: the program's decoding, hoisted out of the loop,
+                                            // runs only here)
+    for (int i = t; i < 16 * MB * 32; i += blockDim.x) {
+      const int row = i >> 5, c = i & 31;
+      const int64_t col = nb[c >> 4] * 16 + (c & 15);
+      if (row < M && (c < 16 || run1_ok))
+        store_out(a.y, a.y_bf16, (yrow0 + row) * a.ldy + col + col_off,
+                  prog_eval(a.prog, fin[row * PLD + c] * scale_s[row], 0, a.row_base + row, col));
+    }
+  } else if (a.P == 1) {  // FH_EP_STORE / FH_EP_RESIDUAL: a thread a column of a row; a run is 16 lanes
     for (int i = t; i < 16 * MB * 32; i += blockDim.x) {
       const int row = i >> 5, c = i & 31, j = c & 15;
       const int64_t run = nb[c >> 4];
@@ -274,7 +286,6 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       const int64_t at = (yrow0 + row) * a.ldy + col + col_off;
       float v = fin[row * PLD + c] * scale_s[row];
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
-      if (kind == FH_EP_PROGRAM && ok) v = prog_eval(a.prog, v, 0, a.row_base + row, col);
       if (ok) store_out(a.y, a.y_bf16, at, v);
       if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) a.copy_bf16[(yrow0 + row) * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
@@ -304,7 +315,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
         store_out(a.y, a.y_bf16, (yrow0 + row) * a.ldy + c0 + col_off, silu(x0) * x1 * scale_s[row]);
       } else {  // FH_EP_ROPE_KV
         const int hd = a.head_dim;
-        const int h = (int)(c0 / hd), d = (int)(c0 % hd), d1 = d + hd / 2;
+        const int h = (int)c0 / hd, d = (int)c0 % hd, d1 = d + hd / 2;  // (c0 < N < 2^31)
         if (h < a.heads + a.kv_heads) {  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
           const int64_t place = rope_place(a, a.places[row]);
           const float* cs = a.cos_tab + place * hd;
