@@ -7,7 +7,10 @@ Prints ONE JSON line: tokens/s of the whole decode step (every kernel of it repl
 in HBM), the dominant GEMV's achieved HBM bandwidth against the 8 TB/s peak (timed live with HIP events on its own
 stream), each GEMV's GB/s, and the CPU baseline: the numpy restatement (oracle/) of one block and the output layer
 timed on this host's cores and scaled to a token; and config 4's prefill (a 2048-token prompt on the matrix cores) as
-its own field, with the same step with every matrix bfp8 (`decode_bfp8`), batches 2-16, and config 5's MoE layer. Synthetic data: random-init weights, drawn on the GPU and packed there."""
+its own field, with the same step with every matrix bfp8 (`decode_bfp8`), batches 2-16, and config 5's MoE layer;
+`configs` holds config 1's GEMV and config 2's SmolLM step on the GPU, and the numpy CPU baselines of configs 1, 2, 4
+and 5 (bounded samples, each saying how it was scaled). Synthetic data: random-init weights, drawn on the GPU and
+packed there."""
 import argparse, json, os, statistics, sys, time
 import numpy as np
 import torch
@@ -221,6 +224,131 @@ def moe_rate(T=32, reps=20):
           "frac": round(nbytes / ms * 1e3 / HBM_PEAK, 4), "tflops": round(flops / ms / 1e9, 1)}
 
 
+def config1_rate(dev, copies=300, reps=10):
+  """Config 1: the bfp8 GEMV x[1,576] @ W[576,1536] (fh_gemv_bfp, fp32 out). Over `copies` distinct packed weights
+  (940,032 bytes each: 282 MB, past the 256 MB Infinity Cache) launched back to back in a HIP graph, so each launch
+  reads its weight from HBM; and the same weight replayed (cache-resident: the launch's latency). Bytes a launch: the
+  packed weight, x (bf16 values held in fp32, 576 x 4) and y (1536 x 4): 947,328 algorithmic bytes as config 1 counts
+  them with x in bf16 (x is 2,304 bytes here, read as fp32)."""
+  from ferrite_amd import ops
+  K, N = 576, 1536
+  g = torch.Generator(device=dev)
+  g.manual_seed(11)
+  ws = [ops.pack(torch.randn(K, N, generator=g, device=dev) * 0.02, "bfp8") for _ in range(copies)]
+  x = torch.randn(1, K, generator=g, device=dev).to(torch.bfloat16).float()
+  y = torch.empty(1, N, device=dev)
+  stream = torch.cuda.Stream(device=dev)
+  def many():
+    for w in ws: ops.gemv(x, w, out=y)
+  ms = timed_graph(many, reps, stream) / copies
+  one = timed_graph(lambda: [ops.gemv(x, ws[0], out=y) for _ in range(copies)], reps, stream) / copies
+  nbytes = K * N * 17 // 16 + K * 2 + N * 4
+  del ws
+  torch.cuda.empty_cache()
+  return {"workload": "config 1: bfp8 GEMV x[1,576] @ W[576,1536], fp32 out", "us": round(ms * 1e3, 3),
+          "gbs": round(nbytes / ms / 1e6, 1), "bytes": nbytes, "copies": copies,
+          "us_cache_resident": round(one * 1e3, 3)}
+
+
+def config2_rate(dev, steps=50, warmup=5, place=143):
+  """Config 2: SmolLM-135M's shape (30 blocks, 576 wide, 9/3 heads of 64, MLP 1536, vocab 49152 tied, bfp8), one
+  token's decode step at place 143 of a bf16 KV cache (128 prompt rows and 16 decoded before it), the whole step one
+  HIP graph replayed between HIP events."""
+  from ferrite_amd import llama as G
+  c, mode, context = config("c2")
+  dec = G.Decoder(c, G.random_weights(c, seed=3, device=dev), mode=mode, kv="bf16", batch=1, context=256)
+  for cache in dec.cache: cache.normal_(0, 1)
+  stream = torch.cuda.Stream(device=dev)
+  with torch.cuda.stream(stream):
+    dec.ids.copy_(torch.tensor([7], dtype=torch.int32))
+    dec.set_rows([place], [0])
+    dec.step(replay=True)
+    for _ in range(warmup): dec.graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps): dec.graph.replay()
+    b.record(stream)
+    b.synchronize()
+  ms = a.elapsed_time(b) / steps
+  nbytes = dec.weight_bytes() + c.layers * 2 * c.kv * dec.hd * (place + 1) * 2
+  del dec
+  torch.cuda.empty_cache()
+  return {"workload": f"config 2: SmolLM-135M-shape decode, batch 1, place {place}, bfp8, bf16 KV", "ms_per_step": round(ms, 4),
+          "tokens_per_s": round(1000 / ms, 1), "step_bytes": nbytes, "step_gbs": round(nbytes / ms / 1e6, 1)}
+
+
+def _median_time(fn, runs):
+  fn()
+  ts = []
+  for _ in range(runs):
+    t0 = time.perf_counter(); fn(); ts.append(time.perf_counter() - t0)
+  return statistics.median(ts)
+
+
+def cpu_configs():
+  """The numpy restatement (oracle/) of configs 1, 2, 4 and 5 on this host's cores, every core BLAS gives, each a
+  bounded sample of the workload timed as benchmark.timed does (median after a warm-up): float32 weights holding the
+  block floats' values (the timing does not depend on the values, so they are drawn in float32 directly)."""
+  from oracle import llama as OL
+  rng = np.random.default_rng(0)
+  f32 = lambda shape, sd=0.02: rng.standard_normal(shape, dtype=np.float32) * np.float32(sd)
+  out = {}
+  # config 1: x @ W (numpy's mm: float32 x float32), GB/s counted on the packed bytes as on the GPU
+  x, w = f32((1, 576), 1.0), f32((576, 1536))
+  t = _median_time(lambda: [x @ w for _ in range(1000)], 5) / 1000
+  out["c1"] = {"us": round(t * 1e6, 3), "gbs": round(947328 / t / 1e9, 2), "unit": "us per GEMV",
+               "sample": "1000 x @ W float32 (numpy sgemv) a run, median of 5"}
+  # config 2: one token through the 30 blocks and the tied output layer at place 143, float64 caches (models/llama.py)
+  c = OL.smollm(layers=30, vocab=49152, places=256)
+  hd, qkv = OL.head(c), (c.heads + 2 * c.kv) * OL.head(c)
+  wts = {"norm": np.ones((1, c.dim), np.float32), "embed": f32((c.vocab, c.dim), 1.0)}
+  wts["embed.T"] = np.ascontiguousarray(wts["embed"].T)
+  for l in range(c.layers):
+    pre = f"layers.{l}."
+    wts |= {pre + "input_layernorm": np.ones((1, c.dim), np.float32), pre + "post_attention_layernorm": np.ones((1, c.dim), np.float32),
+            pre + "qkv_proj": f32((c.dim, qkv)), pre + "o_proj": f32((c.heads * hd, c.dim)),
+            pre + "gate_up_proj": f32((c.dim, 2 * c.ffn)), pre + "down_proj": f32((c.ffn, c.dim))}
+  wts["cos"], wts["sin"], wts["turn"] = OL.rotary(c, c.places)
+  caches = OL.kv_cache(c, 256)
+  for cache in caches: cache[:, :143] = rng.standard_normal(cache[:, :143].shape)
+  t = _median_time(lambda: OL.forward([7], [143], wts, c, caches), 5)
+  out["c2"] = {"tokens_per_s": round(1 / t, 2), "unit": "tokens/s", "sample": "one token at place 143, all 30 blocks, median of 5"}
+  del wts, caches
+  # config 4: one block of the 2048-token prefill (8B shape, float64 caches), scaled by 32 blocks, plus the output layer
+  # for the last token
+  c8 = OL.llama8b(layers=1, places=2048)
+  hd, T = OL.head(c8), 2048
+  p = {"input_layernorm": np.ones((1, c8.dim), np.float32), "post_attention_layernorm": np.ones((1, c8.dim), np.float32),
+       "qkv_proj": f32((c8.dim, (c8.heads + 2 * c8.kv) * hd)), "o_proj": f32((c8.heads * hd, c8.dim)),
+       "gate_up_proj": f32((c8.dim, 2 * c8.ffn)), "down_proj": f32((c8.ffn, c8.dim))}
+  cos, sin, turn = OL.rotary(c8, T)
+  mask = OL.masked(np.arange(T), T)
+  xs = f32((T, c8.dim), 1.0)
+  t = _median_time(lambda: OL.layer(xs, p, c8, (cos, sin, turn), mask, np.zeros((2 * c8.kv, T, hd)), np.arange(T)), 3)
+  head = f32((c8.dim, 128256))
+  th = _median_time(lambda: OL.rms(xs[-1:], p["norm"] if "norm" in p else p["input_layernorm"], c8) @ head, 3)
+  out["c4"] = {"s": round(t * 32 + th, 2), "unit": "s per 2048-token prefill", "scaled": "one block's time x 32 + the output layer",
+               "tokens_per_s": round(T / (t * 32 + th), 1), "sample": "one 8B-shape block over 2048 tokens, median of 3"}
+  del p, head
+  # config 5: the MoE layer for 32 tokens: each (token, chosen expert) pair's SwiGLU (numpy_experts, models/llama.py:294-300)
+  # timed on 8 pairs of one expert's 4096 x 28672 and 14336 x 4096 float32 matrices and scaled to the 64 pairs of
+  # 32 tokens x top 2, plus the router
+  cm = OL.model(dim=4096, k=2, experts=8)
+  gu, dn = f32((4096, 28672)), f32((14336, 4096))
+  h = f32((32, 4096), 1.0)
+  def pairs():
+    for tkn in range(8):
+      g = h[tkn] @ gu
+      OL.glu(g[:14336], g[14336:]) @ dn
+  tp = _median_time(pairs, 3) / 8
+  router = f32((4096, 8))
+  tr = _median_time(lambda: OL.topk(h @ router, 2), 5)
+  out["c5"] = {"ms": round((tp * 64 + tr) * 1e3, 2), "unit": "ms per MoE layer (32 tokens)",
+               "scaled": "8 (token, expert) SwiGLUs timed, x64 pairs, + the router", "sample": "one expert's matrices, median of 3"}
+  return out
+
+
 def measured_traffic(kernel, config, batch):
   """HBM bytes a launch of `kernel` moves, as the committed rocprofv3 counter summaries under profiles/ record them
   (lines `traffic: <kernel> <config> b<batch> <bytes>`: FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's
@@ -412,6 +540,14 @@ def main():
     print(f"# prefill {pre['workload']}: {pre['ms']:.1f} ms, {pre['tokens_per_s']:.0f} tok/s, {pre['tflops']:.0f} TFLOP/s "
           f"({pre['mfma_frac']:.1%} of {MFMA_PEAK / 1e15:.1f} PFLOP/s); gemm {pre['gemm_tflops']}, attention {pre['attention_tflops']} TFLOP/s",
           file=sys.stderr, flush=True)
+  configs = {}
+  if args.config == "c3" and B == 1 and not args.no_prefill:  # configs 1 and 2 on the GPU, beside config 3
+    configs["c1"] = config1_rate(dev)
+    print(f"# {configs['c1']['workload']}: {configs['c1']['us']:.2f} us, {configs['c1']['gbs']:.0f} GB/s over "
+          f"{configs['c1']['copies']} distinct weights ({configs['c1']['us_cache_resident']:.2f} us cache-resident)", file=sys.stderr, flush=True)
+    configs["c2"] = config2_rate(dev)
+    print(f"# {configs['c2']['workload']}: {configs['c2']['ms_per_step']:.3f} ms, {configs['c2']['tokens_per_s']:.0f} tok/s",
+          file=sys.stderr, flush=True)
   cpu = None
   if not args.no_cpu:
     cpu = cpu_baseline(c, mode, context)
@@ -420,6 +556,10 @@ def main():
           f"activations and cache {cpu['float32_tokens_per_s']:.3f} tok/s", file=sys.stderr)
     cpu = {k: (round(cpu[k], 4) if isinstance(cpu[k], float) else cpu[k])
            for k in ("value", "unit", "cores", "kind", "sample", "blas", "one_thread_tokens_per_s", "float32_tokens_per_s")}
+    if args.config == "c3" and B == 1 and not args.no_prefill:
+      for name, v in cpu_configs().items():
+        configs.setdefault(name, {})["cpu"] = v | {"cores": cpu["cores"], "kind": "port"}
+      print("# cpu baselines: " + "; ".join(f"{k} {v['cpu']}" for k, v in configs.items()), file=sys.stderr, flush=True)
   line = {
     "metric": "8B-shape bfp8 decode tok/s @bs1; GEMV HBM GB/s as % of peak",
     "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -440,6 +580,7 @@ def main():
                                                      "frac": round(v["gbs"] * 1e9 / HBM_PEAK, 4)} for k, v in rates8.items()},
     "cpu_baseline": cpu,
     "prefill": pre,
+    "configs": configs,
     **extra,
   }
   print(json.dumps(line), flush=True)
