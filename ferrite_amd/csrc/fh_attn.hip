@@ -31,11 +31,13 @@ struct AttArgs {
   const int32_t* places; const int32_t* first_row;
   int max_chunks;       // the launch's context in chunks (a row reads at most this many)
   int splits;           // S: workgroups a (row, key head), = gridDim.x
-  void* o; int o_bf16;  // the output, fp32 or bf16 (rounded to nearest even)
+  void* o; int o_bf16; int o_tiles;  // the output, fp32 or bf16 (rounded to nearest even), rows or FH_BF16_T16 tiles
+  int64_t o_ld;         // its row length: heads * head_dim
   float* part;          // [batch][heads][splits][hd + 2]: p v, then max, then sum
 };
 
-__device__ inline void put_o(const AttArgs& a, int64_t at, float v) {
+__device__ inline void put_o(const AttArgs& a, int b, int64_t col, float v) {
+  const int64_t at = a.o_tiles ? tile16_at(b, col, a.o_ld) : b * a.o_ld + col;
   if (a.o_bf16) ((uint16_t*)a.o)[at] = (uint16_t)bf16_rne_f(v);
   else ((float*)a.o)[at] = v;
 }
@@ -217,9 +219,9 @@ __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(AttArgs a) {
     __syncthreads();  // the tiles and p are rewritten by the next chunk
   }
   if (parts == 1) {  // the row's only part: o itself
-    const int64_t ob = ((int64_t)b * a.heads + h) * HD + DL * lane;
+    const int64_t ob = (int64_t)h * HD + DL * lane;
 #pragma unroll
-    for (int i = 0; i < DL; ++i) put_o(a, ob + i, o[i] / l);
+    for (int i = 0; i < DL; ++i) put_o(a, b, ob + i, o[i] / l);
     return;
   }
   float* pp = a.part + (((int64_t)b * a.heads + h) * S + split) * (HD + 2);
@@ -405,9 +407,9 @@ __global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
     if (hh >= rep) continue;
     const int64_t h = (int64_t)kvh * rep + hh;
     if (parts == 1) {
-      const int64_t ob = ((int64_t)b * a.heads + h) * HD;
+      const int64_t ob = h * HD;
 #pragma unroll
-      for (int tt = 0; tt < TPW; ++tt) put_o(a, ob + 16 * (w * TPW + tt) + c16, acc_o[tt][i] / l_s[hh]);
+      for (int tt = 0; tt < TPW; ++tt) put_o(a, b, ob + 16 * (w * TPW + tt) + c16, acc_o[tt][i] / l_s[hh]);
     } else {
       float* pp = a.part + (((int64_t)b * a.heads + h) * S + split) * (HD + 2);
 #pragma unroll
@@ -477,7 +479,7 @@ __global__ __launch_bounds__(HD) void attention_combine(AttArgs a) {
     __syncthreads();  // (w_s is rewritten by the next group)
     big = top;
   }
-  put_o(a, ((int64_t)b * a.heads + h) * HD + d, num / den);
+  put_o(a, b, (int64_t)h * HD + d, num / den);
 }
 
 // the kernel, allowed its largest LDS (above 64 KiB for fp32 rows of 256 and 16 heads a key head) once
@@ -603,7 +605,8 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   if (cache_dtype < FH_F32 || cache_dtype > FH_BFP4)
     return fail(FH_EUNSUP, "fh_attention_decode: cache is FH_F32, FH_BF16, FH_BFP8 or FH_BFP4");
   if (max_context < 1 || max_context > cache_len) return fail(FH_EINVAL, "fh_attention_decode: max_context outside 1..cache_len");
-  if (o_dtype != FH_F32 && o_dtype != FH_BF16) return fail(FH_EINVAL, "fh_attention_decode: o is FH_F32 or FH_BF16");
+  if (o_dtype != FH_F32 && o_dtype != FH_BF16 && o_dtype != FH_BF16_T16)
+    return fail(FH_EINVAL, "fh_attention_decode: o is FH_F32, FH_BF16 or FH_BF16_T16");
   const size_t need = fh_attention_workspace_bytes(batch, heads, head_dim, max_context);
   if (max_context > ATT_CHUNK && (!workspace || ws_bytes < need))
     return fail(FH_EINVAL, "fh_attention_decode: workspace smaller than fh_attention_workspace_bytes");
@@ -613,7 +616,7 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
   a.heads = heads; a.kv_heads = kv_heads; a.scale = 1.0f / sqrtf((float)head_dim);
   a.places = places; a.first_row = first_row;
   a.max_chunks = (int)((max_context + ATT_CHUNK - 1) / ATT_CHUNK);
-  a.o = o; a.o_bf16 = o_dtype == FH_BF16;
+  a.o = o; a.o_bf16 = o_dtype != FH_F32; a.o_tiles = o_dtype == FH_BF16_T16; a.o_ld = (int64_t)heads * head_dim;
   a.part = (float*)workspace;
   const int rep = heads / kv_heads;
   // S: workgroups a (row, key head), enough that the grid fills every CU as far as LDS and waves let it (all of it

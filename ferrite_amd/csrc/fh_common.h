@@ -22,6 +22,10 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 __host__ __device__ inline uint32_t bf16_rne(uint32_t b) { return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16; }
 __device__ inline uint32_t bf16_rne_f(float f) { return bf16_rne(__float_as_uint(f)); }
 __device__ inline float bf16_to_f(uint32_t h) { return __uint_as_float(h << 16); }
+// FH_BF16_T16: element (r, c) of bf16 rows of length ld in tiles of 16 rows, 8 columns of the 16 rows together
+__host__ __device__ inline int64_t tile16_at(int64_t r, int64_t c, int64_t ld) {
+  return (r >> 4) * 16 * ld + (c >> 3) * 128 + (r & 15) * 8 + (c & 7);
+}
 
 // One bf16 value's magnitude under a block exponent `top` (>= its own), as models/gpt2.py:25-31 rounds it: q for bfp8
 // (7 bits, half up, at most 127) or for bfp4 (3 bits, nearest with ties up, at most 7, 0 from a shift of 4 on).

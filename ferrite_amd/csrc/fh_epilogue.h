@@ -7,7 +7,7 @@
 namespace fh {
 
 struct MatArgs {
-  const void* x; int64_t ldx; int x_bf16;
+  const void* x; int64_t ldx; int x_bf16; int x_tiles;  // (x_tiles: FH_BF16_T16 rows)
   const uint8_t* mant; const uint8_t* exps; int64_t K; int64_t N; int64_t M;
   int P;                    // runs an item: 1, or 2 for the SiLU·gate and RoPE pairs
   int pair_half;            // P == 2: the runs of a pair are nb0 and nb0 + pair_half
@@ -19,8 +19,8 @@ struct MatArgs {
   const float* norm_w; const float* ssq_in; int ssq_parts; float eps; int centered;
   // epilogue
   int kind;
-  void* y; int64_t ldy; int y_bf16;
-  const float* residual; float* ssq_out; uint16_t* copy_bf16; const float* copy_w;
+  void* y; int64_t ldy; int y_bf16; int y_tiles;
+  const float* residual; float* ssq_out; uint16_t* copy_bf16; const float* copy_w; int copy_tiles;
   int split;
   int heads, kv_heads, head_dim;
   const float* cos_tab; const float* sin_tab; int64_t rope_rows; const int32_t* places; const int32_t* cache_rows;
@@ -34,6 +34,15 @@ __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 __device__ inline void store_out(void* y, int bf16, int64_t at, float v) {
   if (bf16) ((uint16_t*)y)[at] = (uint16_t)bf16_rne_f(v);
   else ((float*)y)[at] = v;
+}
+
+// where output (row, col) of a matmul goes in y, and in the residual epilogue's bf16 copy (row length N)
+__device__ inline int64_t y_at(const MatArgs& a, int64_t row, int64_t col) {
+  return a.y_tiles ? tile16_at(row, col, a.ldy) : row * a.ldy + col;
+}
+__device__ inline void put_copy(const MatArgs& a, int64_t row, int64_t col, float v) {
+  const int64_t at = a.copy_tiles ? tile16_at(row, col, a.N) : row * a.N + col;
+  a.copy_bf16[at] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
 }
 
 // A row's place as an index into the RoPE tables: a place outside them reads their nearest row (the host checks
@@ -131,6 +140,7 @@ inline int epilogue_args(const char* who, const fh_epilogue* ep, int64_t K, int6
       case FH_EP_RESIDUAL:
         if (!ep->residual) return bad(FH_EINVAL, "FH_EP_RESIDUAL needs residual");
         a.residual = ep->residual; a.ssq_out = ep->ssq_out; a.copy_bf16 = (uint16_t*)ep->copy_bf16; a.copy_w = ep->copy_w;
+        a.copy_tiles = ep->copy_bf16 && ep->copy_tiles;
         if (y_dtype != FH_F32) return bad(FH_EUNSUP, "FH_EP_RESIDUAL writes fp32");
         break;
       case FH_EP_SILU_GATE:

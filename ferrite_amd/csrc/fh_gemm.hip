@@ -271,7 +271,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
       float v = Cs[r * GM_LDC + c] * rs_s[r];
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
       if (ok) store_out(a.y, a.y_bf16, at, v);
-      if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) a.copy_bf16[m * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
+      if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) put_copy(a, m, col, v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;
         s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
@@ -356,20 +356,25 @@ extern "C" int fh_gemm_bfp(const void* x, int x_dtype, int64_t ldx, int64_t M, i
   if (!x || !w_mant || !w_exps || !y) return fail(FH_EINVAL, "fh_gemm_bfp: null pointer");
   if (M < 1 || K < 32 || K % 32 || N < 16 || N % 16)
     return fail(FH_EINVAL, "fh_gemm_bfp: need M >= 1, K a multiple of 32, N a multiple of 16");
-  if (x_dtype != FH_F32 && x_dtype != FH_BF16) return fail(FH_EINVAL, "fh_gemm_bfp: x is FH_F32 or FH_BF16");
-  if (y_dtype != FH_F32 && y_dtype != FH_BF16) return fail(FH_EINVAL, "fh_gemm_bfp: y is FH_F32 or FH_BF16");
+  if (x_dtype != FH_F32 && x_dtype != FH_BF16 && x_dtype != FH_BF16_T16)
+    return fail(FH_EINVAL, "fh_gemm_bfp: x is FH_F32, FH_BF16 or FH_BF16_T16");
+  if (y_dtype != FH_F32 && y_dtype != FH_BF16 && y_dtype != FH_BF16_T16)
+    return fail(FH_EINVAL, "fh_gemm_bfp: y is FH_F32, FH_BF16 or FH_BF16_T16");
   if (fmt != FH_BFP8 && fmt != FH_BFP4) return fail(FH_EINVAL, "fh_gemm_bfp: fmt is FH_BFP8 or FH_BFP4");
   if (ldx < K || ldx % 8) return fail(FH_EINVAL, "fh_gemm_bfp: ldx < K or not a multiple of 8 (16-byte row loads)");
   MatArgs a = {};
-  a.x = x; a.ldx = ldx; a.x_bf16 = x_dtype == FH_BF16;
+  a.x = x; a.ldx = ldx; a.x_bf16 = x_dtype != FH_F32; a.x_tiles = x_dtype == FH_BF16_T16;
   a.mant = (const uint8_t*)w_mant; a.exps = w_exps; a.K = K; a.N = N; a.M = M;
-  a.y = y; a.y_bf16 = y_dtype == FH_BF16; a.ldy = ldy;
+  a.y = y; a.y_bf16 = y_dtype != FH_F32; a.y_tiles = y_dtype == FH_BF16_T16; a.ldy = ldy;
   if (int rc = epilogue_args("fh_gemm_bfp", ep, K, N, y_dtype, ldy, a)) return rc;
+  if (a.y_tiles && ldy % 8) return fail(FH_EINVAL, "fh_gemm_bfp: FH_BF16_T16 y needs ldy a multiple of 8");
   hipStream_t s = as_stream(stream);
   if (M <= 64 && K % 64 == 0) {  // a few rows: the skinny kernel (K split among waves, as the GEMV splits it)
     const SkinnyMoe none = {};
     return skinny_matmul(a, none, fmt, 1, s);
   }
+  if (a.x_tiles || a.y_tiles || a.copy_tiles)
+    return fail(FH_EUNSUP, "fh_gemm_bfp: FH_BF16_T16 rows (and copy_tiles) are for up to 64 rows with K a multiple of 64");
   const SkinnyMoe none = {};
   if (int rc = gemm_tiles(a, none, fmt, 1, s)) return rc;
   return check_launch("fh_gemm_bfp");

@@ -160,7 +160,7 @@ __global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(MatArgs a) {
       float v = fin[i] * rs[b];
       if (kind == FH_EP_RESIDUAL) v += a.residual[at];
       store_out(a.y, a.y_bf16, at, v);
-      if (kind == FH_EP_RESIDUAL && a.copy_bf16) a.copy_bf16[b * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
+      if (kind == FH_EP_RESIDUAL && a.copy_bf16) put_copy(a, a.copy_tiles ? a.row_base + b : b, col, v);  // (tiles: rows from the call's first)
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;
         s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
@@ -301,7 +301,7 @@ extern "C" int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, i
     c.y = (char*)y + (size_t)b0 * ldy * (a.y_bf16 ? 2 : 4);
     if (c.ssq_in) c.ssq_in += (int64_t)b0 * c.ssq_parts;
     if (c.residual) c.residual += (int64_t)b0 * ldy;
-    if (c.copy_bf16) c.copy_bf16 += (int64_t)b0 * N;
+    if (c.copy_bf16 && !c.copy_tiles) c.copy_bf16 += (int64_t)b0 * N;
     if (c.ssq_out) c.ssq_out += (int64_t)b0 * (N / 16);
     if (c.places) { c.places += b0; c.cache_rows += b0; }
     if (c.argmax_parts) c.argmax_parts += (int64_t)b0 * (N / 16);

@@ -205,14 +205,14 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
 // out = x * rsqrt(mean(x^2) + eps) * w (w + 1 when centered), a workgroup a row (models/llama.py:82-85)
 template <bool OBF16>
 __global__ __launch_bounds__(256) void rms_rows_kernel(const float* x, int64_t ldx, int dim, const float* w, float eps,
-                                                       int centered, void* out, int64_t ldo) {
+                                                       int centered, void* out, int64_t ldo, int tiles) {
   const int64_t row = blockIdx.x;
   const float* xr = x + row * ldx;
   __shared__ float part[4];
   auto put = [&](int i, float xi, float rs) {
     const float g = centered ? w[i] + 1.f : w[i];
     const float v = xi * rs * g;
-    if (OBF16) ((uint16_t*)out)[row * ldo + i] = (uint16_t)bf16_rne_f(v);
+    if (OBF16) ((uint16_t*)out)[tiles ? tile16_at(row, i, ldo) : row * ldo + i] = (uint16_t)bf16_rne_f(v);
     else ((float*)out)[row * ldo + i] = v;
   };
   constexpr int R = 16;  // values a thread holds for a row of up to 256 R: all its loads issued at once, read once
@@ -290,10 +290,13 @@ extern "C" int fh_rms_rows(const float* x, int64_t ldx, int64_t rows, int64_t di
                            int centered, void* out, int out_dtype, int64_t ldo, void* stream) {
   if (!x || !norm_w || !out) return fail(FH_EINVAL, "fh_rms_rows: null pointer");
   if (rows < 1 || dim < 1 || ldx < dim || ldo < dim) return fail(FH_EINVAL, "fh_rms_rows: need rows, dim >= 1, ldx and ldo >= dim");
-  if (out_dtype != FH_F32 && out_dtype != FH_BF16) return fail(FH_EINVAL, "fh_rms_rows: out is FH_F32 or FH_BF16");
+  if (out_dtype != FH_F32 && out_dtype != FH_BF16 && out_dtype != FH_BF16_T16)
+    return fail(FH_EINVAL, "fh_rms_rows: out is FH_F32, FH_BF16 or FH_BF16_T16");
+  const int tiles = out_dtype == FH_BF16_T16;
+  if (tiles && ldo % 8) return fail(FH_EINVAL, "fh_rms_rows: FH_BF16_T16 out needs ldo a multiple of 8");
   if (rows >= (1LL << 31)) return fail(FH_EUNSUP, "fh_rms_rows: too many rows");
   hipStream_t s = as_stream(stream);
-  if (out_dtype == FH_BF16) hipLaunchKernelGGL((rms_rows_kernel<true>), dim3((unsigned)rows), dim3(256), 0, s, x, ldx, (int)dim, norm_w, eps, centered, out, ldo);
-  else hipLaunchKernelGGL((rms_rows_kernel<false>), dim3((unsigned)rows), dim3(256), 0, s, x, ldx, (int)dim, norm_w, eps, centered, out, ldo);
+  if (out_dtype != FH_F32) hipLaunchKernelGGL((rms_rows_kernel<true>), dim3((unsigned)rows), dim3(256), 0, s, x, ldx, (int)dim, norm_w, eps, centered, out, ldo, tiles);
+  else hipLaunchKernelGGL((rms_rows_kernel<false>), dim3((unsigned)rows), dim3(256), 0, s, x, ldx, (int)dim, norm_w, eps, centered, out, ldo, 0);
   return check_launch("fh_rms_rows");
 }

@@ -9,7 +9,9 @@
 // row-major into the wave's own LDS tile (no workgroup barrier in the loop: a wave reads back only what it wrote);
 // ds_read_b64_tr_b16 then reads the tile back K-contiguous, as v_mfma_f32_16x16x32_bf16 takes its operand (in each
 // 16-lane group, lane 4m + q addresses row m, columns 4q .. 4q + 3; lane j receives column j of the four rows). x's
-// rows (16 a block, up to 4 blocks) come straight from memory, 8 consecutive k a lane, a step ahead. The waves' sums
+// rows (16 a block, up to 4 blocks) come straight from memory, 8 consecutive k a lane, a step ahead: a wave's load
+// takes 16 rows' 64 bytes from rows, 1 KiB in one piece from bf16 tiles of 16 rows (FH_BF16_T16), which a decode step
+// of many sequences passes between its kernels (down's 33 MB of bfp4 at batch 16: 21.5 us from rows, ~17 from tiles). The waves' sums
 // then meet in LDS in a fixed order and the epilogue runs on the item's outputs.
 //
 // For a mixture of experts the grid's second dimension is the expert: the weight is the expert's (`expert_mant` /
@@ -123,11 +125,15 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       mrun[j] = mant + run * a.K * RB;
       erun[j] = exps + run * a.K;
     }
-    // x: row 16 b + lane % 16, k 8 (lane / 16) .. + 7 of each 32 k
+    // x: row 16 b + lane % 16, k 8 (lane / 16) .. + 7 of each 32 k. In rows, a wave's 16-byte loads take 16 rows'
+    // 64 bytes each (rows past M read row M - 1); in tiles of 16 rows (FH_BF16_T16, bf16), 1 KiB in a piece
+    const bool tiles = XBF16 && a.x_tiles;
     const char* xp[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b)
-      xp[b] = (const char*)a.x + (xrow(min(16 * b + (lane & 15), M - 1)) * a.ldx + (int64_t)e * moe.expert_xcols + 8 * (lane >> 4)) * (XBF16 ? 2 : 4);
+      xp[b] = tiles ? (const char*)a.x + ((int64_t)16 * b * a.ldx + 8 * lane) * 2
+                    : (const char*)a.x + (xrow(min(16 * b + (lane & 15), M - 1)) * a.ldx + (int64_t)e * moe.expert_xcols + 8 * (lane >> 4)) * (XBF16 ? 2 : 4);
+    const int xk = tiles ? 32 : XBF16 ? 2 : 4;  // bytes a column of k moves the loads on
     const int last = r1 - SK_BK;  // (r1 - r0 is a multiple of 64: K is)
     // the transposed reads' addresses in the tile: 16-lane group g reads k 8 (g / 2)... of the 32-k block; in the
     // group, lane 4 m + q points at row m, columns 4 q .. 4 q + 3 of the run
@@ -151,7 +157,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       for (int b = 0; b < MB; ++b)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const uint4* p = (const uint4*)(xp[b] + (int64_t)(k0 + 32 * h) * (XBF16 ? 2 : 4));
+          const uint4* p = (const uint4*)(xp[b] + (int64_t)(k0 + 32 * h) * xk);
 #pragma unroll
           for (int i = 0; i < XW; ++i) xs[b][h][i] = p[i];
         }
@@ -274,7 +280,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       const int row = i >> 5, c = i & 31;
       const int64_t col = nb[c >> 4] * 16 + (c & 15);
       if (row < M && (c < 16 || run1_ok))
-        store_out(a.y, a.y_bf16, (yrow0 + row) * a.ldy + col + col_off,
+        store_out(a.y, a.y_bf16, y_at(a, yrow0 + row, col + col_off),
                   prog_eval(a.prog, fin[row * PLD + c] * scale_s[row], 0, a.row_base + row, col));
     }
   } else if (a.P == 1) {  // FH_EP_STORE / FH_EP_RESIDUAL: a thread a column of a row; a run is 16 lanes
@@ -286,8 +292,8 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       const int64_t at = (yrow0 + row) * a.ldy + col + col_off;
       float v = fin[row * PLD + c] * scale_s[row];
       if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
-      if (ok) store_out(a.y, a.y_bf16, at, v);
-      if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) a.copy_bf16[(yrow0 + row) * a.N + col] = (uint16_t)bf16_rne_f(a.copy_w ? v * a.copy_w[col] : v);
+      if (ok) store_out(a.y, a.y_bf16, y_at(a, yrow0 + row, col + col_off), v);  // (RESIDUAL's y is rows: at)
+      if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) put_copy(a, yrow0 + row, col, v);
       if (kind == FH_EP_RESIDUAL && a.ssq_out) {
         float s = v * v;
         s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
@@ -312,7 +318,7 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
       float x0 = fin[row * PLD + j], x1 = fin[row * PLD + 16 + j];
       const int64_t c0 = nb[0] * 16 + j;
       if (kind == FH_EP_SILU_GATE) {
-        store_out(a.y, a.y_bf16, (yrow0 + row) * a.ldy + c0 + col_off, silu(x0) * x1 * scale_s[row]);
+        store_out(a.y, a.y_bf16, y_at(a, yrow0 + row, c0 + col_off), silu(x0) * x1 * scale_s[row]);
       } else {  // FH_EP_ROPE_KV
         const int hd = a.head_dim;
         const int h = (int)c0 / hd, d = (int)c0 % hd, d1 = d + hd / 2;  // (c0 < N < 2^31)

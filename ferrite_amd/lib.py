@@ -7,7 +7,7 @@ import ctypes, os, pathlib
 HERE = pathlib.Path(__file__).resolve().parent
 PATH = pathlib.Path(os.environ.get("FERRITE_HIP_LIB", HERE / "libferrite_hip.so"))
 
-F32, BF16, BFP8, BFP4, I32 = 0, 1, 2, 3, 4
+F32, BF16, BFP8, BFP4, I32, BF16_T16 = 0, 1, 2, 3, 4, 5
 AXIS_N, AXIS_K = 0, 1
 EP_STORE, EP_RESIDUAL, EP_SILU_GATE, EP_ROPE_KV, EP_PROGRAM = 0, 1, 2, 3, 4
 MAX_OPS, MAX_INPUTS = 15, 8
@@ -38,7 +38,7 @@ class Epilogue(ctypes.Structure):
               ("residual", P), ("ssq_out", P), ("split", I), ("heads", I), ("kv_heads", I), ("head_dim", I),
               ("cos_tab", P), ("sin_tab", P), ("places", P), ("cache_rows", P), ("cache", P), ("cache_dtype", I),
               ("cache_len", L), ("argmax_parts", P), ("program", ctypes.POINTER(Program)), ("copy_bf16", P), ("copy_w", P),
-              ("rope_rows", L)]
+              ("rope_rows", L), ("copy_tiles", I)]
 
 
 SIGNATURES = {

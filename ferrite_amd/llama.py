@@ -151,9 +151,12 @@ class Decoder:
     self.x, self.ssq = z(B, c.dim), z(B, c.dim // 16)
     self.q, self.att = z(B, c.heads * hd), z(B, c.heads * hd)
     self.h = z(B, c.ffn)
-    self.xn = torch.zeros(B, c.dim, dtype=torch.bfloat16, device=self.device)   # the matrix cores' bf16 rows (each residual epilogue's copy)
-    self.hb = torch.zeros(B, c.ffn, dtype=torch.bfloat16, device=self.device)
-    self.attb = torch.zeros(B, c.heads * hd, dtype=torch.bfloat16, device=self.device)  # attention's rows for o's matrix cores
+    # the matrix cores' bf16 rows: each residual epilogue's copy, SwiGLU's output, attention's output for o; in tiles of
+    # 16 rows (FH_BF16_T16) up to 64 rows, which the matrix-core kernel for a few rows loads a whole line at a time
+    rows16 = ops.tiles16 if B <= 64 else (lambda r, n, d: torch.zeros(r, n, dtype=torch.bfloat16, device=d))
+    self.xn = rows16(B, c.dim, self.device)
+    self.hb = rows16(B, c.ffn, self.device)
+    self.attb = rows16(B, c.heads * hd, self.device)
     self.logits = z(B, c.vocab)
     self.picks = torch.zeros(B, dtype=torch.int32, device=self.device)
     self.parts = torch.zeros(B, c.vocab // 16, dtype=torch.int64, device=self.device)  # each run of 16 logits' best

@@ -96,12 +96,56 @@ def dequant(bw, out=None):
   return out
 
 
+@dataclass
+class Tiles16:
+  """bf16 rows [rows][cols] in tiles of 16 rows (FH_BF16_T16): element (r, c) at (r // 16) * 16 * cols + (c // 8) * 128
+  + (r % 16) * 8 + c % 8 of `data`, which holds 16 * ceil(rows / 16) rows. The rows a decode step of many sequences
+  passes between its matrix-core matmuls (each 16 rows' 8 columns one contiguous 256-byte piece)."""
+  data: torch.Tensor
+  rows: int
+  cols: int
+
+  @property
+  def dtype(self): return "bf16_t16"
+
+  def rows_(self):
+    """The rows as a [rows][cols] bf16 tensor (a copy)."""
+    r16 = -(-self.rows // 16) * 16
+    t = self.data.view(r16 // 16, self.cols // 8, 16, 8).permute(0, 2, 1, 3).reshape(r16, self.cols)
+    return t[:self.rows].contiguous()
+
+
+def tiles16(rows, cols, device="cuda", fill=0.0):
+  """Zeros (or `fill`) as bf16 tiles of 16 rows: [rows][cols], cols a multiple of 8."""
+  if cols % 8: raise ValueError("tiles16: cols a multiple of 8")
+  r16 = -(-rows // 16) * 16
+  return Tiles16(torch.full((r16 * cols,), fill, dtype=torch.bfloat16, device=device), rows, cols)
+
+
+def to_tiles16(x, fill=0.0):
+  """A [rows][cols] tensor's values as bf16 tiles of 16 rows (the rows past `rows` in the last tile hold `fill`)."""
+  rows, cols = x.shape
+  t = tiles16(rows, cols, x.device, fill)
+  r16 = -(-rows // 16) * 16
+  full = torch.full((r16, cols), fill, dtype=torch.bfloat16, device=x.device)
+  full[:rows] = x.to(torch.bfloat16)
+  t.data.copy_(full.view(r16 // 16, 16, cols // 8, 8).permute(0, 2, 1, 3).reshape(-1))
+  return t
+
+
 def epilogue(kind=lib.EP_STORE, **kw):
-  """An fh_epilogue; tensors given are kept alive with it (the kernel reads them when it runs, after this returns)."""
+  """An fh_epilogue; tensors given are kept alive with it (the kernel reads them when it runs, after this returns). A
+  Tiles16 copy_bf16 sets copy_tiles."""
   ep = lib.Epilogue()
   ep.kind = kind
   ep.keep = []
   for k, v in kw.items():
+    if isinstance(v, Tiles16):
+      if k != "copy_bf16": raise ValueError(f"epilogue: {k} cannot be bf16 tiles")
+      _dev(v.data)
+      ep.keep.append(v.data)
+      ep.copy_tiles = 1
+      v = v.data.data_ptr()
     if isinstance(v, torch.Tensor):
       _dev(v)
       ep.keep.append(v)
@@ -110,20 +154,30 @@ def epilogue(kind=lib.EP_STORE, **kw):
   return ep
 
 
+def _layout(t):
+  """(pointer, dtype code, row stride, rows) of a matmul operand: a [rows][cols] tensor or bf16 tiles of 16 rows."""
+  if isinstance(t, Tiles16):
+    _dev(t.data)
+    return t.data.data_ptr(), lib.BF16_T16, t.cols, t.rows
+  _dev(t)
+  return _ptr(t), _TORCH[t.dtype], t.stride(0), t.shape[0]
+
+
 def _matmul(entry, x, bw, ep, out, out_dtype):
-  _dev(x)
   if bw.axis != lib.AXIS_N: raise NotImplementedError(f"{entry}: weights packed along N")
-  if x.dim() != 2 or x.shape[1] != bw.K or x.stride(1) != 1: raise ValueError(f"{entry}: x {tuple(x.shape)} for W {bw.K}x{bw.N}")
-  rows = x.shape[0]
+  if isinstance(x, Tiles16):
+    if x.cols != bw.K: raise ValueError(f"{entry}: x tiles of {x.cols} columns for W {bw.K}x{bw.N}")
+  elif x.dim() != 2 or x.shape[1] != bw.K or x.stride(1) != 1: raise ValueError(f"{entry}: x {tuple(x.shape)} for W {bw.K}x{bw.N}")
+  xp, xdt, ldx, rows = _layout(x)
   if out is None:
     cols = bw.N
     if ep is not None and ep.kind == lib.EP_SILU_GATE: cols = ep.split
     if ep is not None and ep.kind == lib.EP_ROPE_KV: cols = ep.heads * ep.head_dim
-    out = torch.empty(rows, cols, dtype=out_dtype, device=x.device)
-  _dev(out)
-  lib.call(entry, _ptr(x), _TORCH[x.dtype], x.stride(0), rows, bw.K, bw.N, _ptr(bw.mant), _ptr(bw.exps),
-           lib.DTYPES[bw.fmt], ctypes.byref(ep) if ep is not None else None, _ptr(out), _TORCH[out.dtype], out.stride(0),
-           _stream())
+    dev = x.data.device if isinstance(x, Tiles16) else x.device
+    out = torch.empty(rows, cols, dtype=out_dtype, device=dev)
+  yp, ydt, ldy, _ = _layout(out)
+  lib.call(entry, xp, xdt, ldx, rows, bw.K, bw.N, _ptr(bw.mant), _ptr(bw.exps),
+           lib.DTYPES[bw.fmt], ctypes.byref(ep) if ep is not None else None, yp, ydt, ldy, _stream())
   return out
 
 
@@ -133,7 +187,8 @@ def gemv(x, bw, ep=None, out=None, out_dtype=torch.float32):
 
 
 def gemm(x, bw, ep=None, out=None, out_dtype=torch.float32):
-  """y = x @ W with the epilogue ep (fh_gemm_bfp): many rows on the matrix cores, x (fp32 or bf16) rounded to bf16."""
+  """y = x @ W with the epilogue ep (fh_gemm_bfp): many rows on the matrix cores, x (fp32 or bf16) rounded to bf16. x
+  and out may be Tiles16 (up to 64 rows, K a multiple of 64)."""
   return _matmul("fh_gemm_bfp", x, bw, ep, out, out_dtype)
 
 
@@ -199,15 +254,18 @@ def attention_workspace(batch, heads, head_dim, max_context, device="cuda"):
 
 def attention_decode(q, cache, heads, kv_heads, head_dim, places, first_row, max_context, workspace, o=None):
   """softmax(q k^T / sqrt(hd)) v over each row's cache rows (fh_attention_decode). cache [2 kv][len][hd] (fp32, bf16 or
-  a BfpCache); o fp32 (by default) or bf16."""
+  a BfpCache); o fp32 (by default) or bf16, or bf16 Tiles16 of q's shape."""
   data, dtype, length = cache_fields(cache)
   _dev(q, data, places, first_row)
   batch = q.shape[0]
   if o is None: o = torch.empty_like(q)
-  if o.dtype not in (torch.float32, torch.bfloat16) or o.shape != q.shape or not o.is_contiguous():
+  if isinstance(o, Tiles16):
+    if (o.rows, o.cols) != tuple(q.shape): raise ValueError("attention_decode: o tiles of q's shape")
+  elif o.dtype not in (torch.float32, torch.bfloat16) or o.shape != q.shape or not o.is_contiguous():
     raise ValueError("attention_decode: o is a contiguous fp32 or bf16 tensor of q's shape")
+  op, odt, _, _ = _layout(o)
   lib.call("fh_attention_decode", _ptr(q), _ptr(data), dtype, length, batch, heads, kv_heads, head_dim, _ptr(places),
-           _ptr(first_row), max_context, _ptr(o), _TORCH[o.dtype], _ptr(workspace), workspace.numel(), _stream())
+           _ptr(first_row), max_context, op, odt, _ptr(workspace), workspace.numel(), _stream())
   return o
 
 
@@ -225,12 +283,13 @@ def attention_prefill(q, cache, heads, kv_heads, head_dim, p0, slot_row, o=None,
 
 
 def rms_rows(x, w, eps, centered=False, out=None, out_dtype=torch.bfloat16):
-  """x * rsqrt(mean(x^2) + eps) * w, a row at a time (fh_rms_rows); bf16 out by default (a prefill GEMM's input)."""
+  """x * rsqrt(mean(x^2) + eps) * w, a row at a time (fh_rms_rows); bf16 out by default (a prefill GEMM's input), or
+  bf16 Tiles16."""
   _dev(x, w)
   if out is None: out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
-  _dev(out)
-  lib.call("fh_rms_rows", _ptr(x), x.stride(0), x.shape[0], x.shape[1], _ptr(w), eps, int(centered), _ptr(out),
-           _TORCH[out.dtype], out.stride(0), _stream())
+  op, odt, ldo, _ = _layout(out)
+  lib.call("fh_rms_rows", _ptr(x), x.stride(0), x.shape[0], x.shape[1], _ptr(w), eps, int(centered), op, odt, ldo,
+           _stream())
   return out
 
 

@@ -34,6 +34,14 @@ extern "C" {
 #define FH_BFP8 2
 #define FH_BFP4 3
 #define FH_I32 4
+/* bf16 rows in tiles of 16 rows: element (r, c) of rows of length ld (a multiple of 8) sits at
+ * (r / 16) * 16 * ld + (c / 8) * 128 + (r % 16) * 8 + c % 8, so that 8 columns of 16 rows are 256 contiguous bytes,
+ * and a buffer of M rows holds 16 * ceil(M / 16) rows (the rows past M are read and never used). The layout of the
+ * bf16 rows that pass between the kernels of a decode step of 3 to 64 sequences: fh_gemm_bfp's matrix-core kernel for
+ * up to 64 rows loads x's 8 columns of 16 rows in one wave-wide read of whole lines where a row-major x takes 16 half
+ * lines. Taken as fh_gemm_bfp's x and y (up to 64 rows, K a multiple of 64), attention's o and fh_rms_rows' out, and
+ * written by FH_EP_RESIDUAL's copy (copy_tiles). No counterpart in the reference (a device layout). */
+#define FH_BF16_T16 5
 
 /* which axis of a weight W[K][N] (x @ W, K rows, N columns) a block of 16 values runs along:
  * FH_AXIS_N, along a row (16 consecutive columns share an exponent): ferrite's own, gpt2.bfp on W (models/gpt2.py:27,
@@ -149,6 +157,9 @@ typedef struct fh_epilogue {
    * the nearest row, and a cache row outside 0 .. cache_len - 1 is not written: the caller checks both, these keep a
    * bad value from reading or writing past the buffers. */
   int64_t rope_rows;
+  /* FH_EP_RESIDUAL's copy_bf16 in tiles of 16 rows (FH_BF16_T16, row length N) rather than rows: nonzero for the
+   * matrix-core kernel's x (fh_gemm_bfp, up to 64 rows) */
+  int copy_tiles;
 } fh_epilogue;
 
 /* y (dtype y_dtype, row stride ldy) from x @ W and the epilogue. x: fp32. w_mant/w_exps: a packed [K][N] weight
