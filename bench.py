@@ -2,6 +2,7 @@
 attention and the output layer in bfp8, every MLP matrix in bfp4, a bf16 KV cache at context 2048, batch 1).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c3-bfp8|c2] [--batch B] [--no-cpu] [--no-prefill]
+                [--only bs16|prefill|moe|floor]
 
 Prints ONE JSON line: tokens/s of the whole decode step (every kernel of it replayed as one HIP graph, inputs resident
 in HBM), the dominant GEMV's achieved HBM bandwidth against the 8 TB/s peak (timed live with HIP events on its own
@@ -10,7 +11,8 @@ timed on this host's cores and scaled to a token; and config 4's prefill (a 2048
 its own field, with the same step with every matrix bfp8 (`decode_bfp8`), batches 2-16, and config 5's MoE layer;
 `configs` holds config 1's GEMV and config 2's SmolLM step on the GPU, and the numpy CPU baselines of configs 1, 2, 4
 and 5 (bounded samples, each saying how it was scaled). Synthetic data: random-init weights, drawn on the GPU and
-packed there."""
+packed there. --only runs one part by itself and prints its fields as the JSON line (what a profiler run of one part
+uses): the batch-16 step, config 4's prefill, config 5's MoE layer, or the read floor (read_floor)."""
 import argparse, json, os, statistics, sys, time
 import numpy as np
 import torch
@@ -360,6 +362,34 @@ def measured_traffic(kernel, config, batch):
   return None
 
 
+def read_floor(dev, reps=5):
+  """What a plain read of each batch-1 GEMV's bytes takes, launched as the step launches a GEMV: a graph of 32 launches
+  back to back over 32 distinct buffers (each read from HBM), each launch fh_read_probe (16-byte loads, four in flight
+  a thread, the fastest of 1024-8192 workgroups of 256 threads: every byte read once, nothing else done), timed by HIP events on the
+  stream: the floor a kernel of that many bytes meets before any arithmetic. Sizes: the 8B shapes' packed weights
+  (magnitudes and exponents) of qkv and o (bfp8), gate_up and down (bfp4), and the all-bfp8 gate_up and down."""
+  from ferrite_amd import lib
+  sizes = {"qkv bfp8": 4096 * 6144 * 17 // 16, "o bfp8": 4096 * 4096 * 17 // 16, "down bfp4": 14336 * 4096 * 9 // 16,
+           "gate_up bfp4": 4096 * 28672 * 9 // 16, "down bfp8": 14336 * 4096 * 17 // 16, "gate_up bfp8": 4096 * 28672 * 17 // 16}
+  stream = torch.cuda.Stream(device=dev)
+  sink = torch.empty(8192, dtype=torch.int32, device=dev)
+  out = {}
+  for name, nbytes in sizes.items():
+    n = (nbytes + 15) // 16 * 16
+    bufs = [torch.ones(n // 4, device=dev) for _ in range(32)]
+    best = None
+    for blocks in (1024, 2048, 4096, 8192):  # (the fastest grid of each size)
+      def run():
+        for t in bufs: lib.call("fh_read_probe", t.data_ptr(), n, sink.data_ptr(), blocks, torch.cuda.current_stream().cuda_stream)
+      ms = timed_graph(run, reps, stream) / 32
+      if best is None or ms < best[0]: best = (ms, blocks)
+    ms, blocks = best
+    out[name] = {"bytes": n, "us": round(ms * 1e3, 3), "gbs": round(n / ms / 1e6, 1), "blocks": blocks}
+    del bufs
+  torch.cuda.empty_cache()
+  return out
+
+
 def measured_peaks(dev, reps=10):
   """What this GPU reaches on plain library kernels, beside the published peaks: HBM read (torch.sum of 2 GiB of fp32
   by rows of 1024, every byte read once: the fastest of the reductions tried, ~6.4 TB/s) and copy (torch.neg, 2 GiB in and out), and a large bf16 GEMM on the matrix cores
@@ -449,6 +479,7 @@ def main():
   ap.add_argument("--batch", type=int, default=1)
   ap.add_argument("--no-cpu", action="store_true")
   ap.add_argument("--no-prefill", action="store_true", help="skip config 4's prefill measurement")
+  ap.add_argument("--only", choices=("bs16", "prefill", "moe", "floor"), help="run one part alone (see above)")
   ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                   help="first run a plain copy kernel (torch.neg) over MIB MiB: the known-size kernel that calibrates "
                        "rocprofv3's FETCH_SIZE/WRITE_SIZE counters in the same run")
@@ -468,6 +499,15 @@ def main():
     torch.cuda.synchronize()
     del src, dst
   c, mode, context = config(args.config)
+  if args.only:
+    if args.only == "bs16":
+      dec = G.Decoder(c, G.random_weights(c, seed=1, device=dev), mode=mode, kv="bf16", batch=1, context=context)
+      r = decode_batch(dec, context)
+    elif args.only == "prefill": r = prefill_rate()
+    elif args.only == "moe": r = {"moe": moe_rate(), "moe_prompt": moe_rate(2048, reps=5)}
+    else: r = read_floor(dev)
+    print(json.dumps({"only": args.only, **r}), flush=True)
+    return
   t0 = time.time()
   dec = G.Decoder(c, G.random_weights(c, seed=1, device=dev), mode=mode, kv="bf16", batch=args.batch, context=context,
                   slots=args.batch)
@@ -500,6 +540,9 @@ def main():
         file=sys.stderr, flush=True)
   for k, r in rates.items():
     print(f"# gemv {k:8s} {r['fmt']} {r['K']}x{r['N']}: {r['us']:.2f} us, {r['gbs']:.0f} GB/s ({r['gbs'] * 1e9 / HBM_PEAK:.1%})", file=sys.stderr, flush=True)
+  floor = read_floor(dev) if args.config == "c3" and B == 1 else None
+  if floor: print("# read floor (32 distinct buffers a graph): " + ", ".join(f"{k} {v['us']:.2f} us" for k, v in floor.items()),
+                  file=sys.stderr, flush=True)
   rates8 = None
   extra = {}
   if args.config == "c3" and B == 1:  # the target's own kernels: the 8B shapes with every matrix bfp8
@@ -576,6 +619,9 @@ def main():
     "measured_peaks": peaks,
     "gemv_gbs": {k: round(v["gbs"], 1) for k, v in rates.items()},
     "gemv_us": {k: round(v["us"], 3) for k, v in rates.items()},
+    "read_floor": floor,
+    "gemv_of_floor": None if floor is None else {k: round(floor[f"{k} {rates[k]['fmt']}"]["us"] / rates[k]["us"], 3)
+                                                 for k in ("qkv", "o", "gate_up", "down")},
     "gemv_bfp8_8b": None if rates8 is None else {k: {"us": round(v["us"], 3), "gbs": round(v["gbs"], 1),
                                                      "frac": round(v["gbs"] * 1e9 / HBM_PEAK, 4)} for k, v in rates8.items()},
     "cpu_baseline": cpu,

@@ -285,3 +285,30 @@ extern "C" int fh_argmax_parts(const void* parts, int64_t rows, int64_t nparts, 
   hipLaunchKernelGGL(argmax_parts_kernel, dim3((unsigned)rows), dim3(AP_T), 0, as_stream(stream), (const int2*)parts, nparts, ids);
   return check_launch("fh_argmax_parts");
 }
+
+// The read floor a matmul's stream is measured against: `bytes` read once, 16 bytes a load, four loads in flight a
+// thread, in a grid-stride walk of `blocks` workgroups of 256 threads; each workgroup's xor of every word it read
+// goes to sink[block] (so that the loads are used)
+__global__ __launch_bounds__(256) void read_probe_kernel(const uint4* src, int64_t n16, uint32_t* sink) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  }
+  for (; i < n16; i += stride) { const uint4 a = src[i]; acc ^= a.x ^ a.y ^ a.z ^ a.w; }
+  for (int m = 32; m >= 1; m >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, m, 64);
+  __shared__ uint32_t part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+}
+
+extern "C" int fh_read_probe(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream) {
+  if (!src || !sink || bytes < 16 || bytes % 16 || blocks < 1 || blocks > 65536)
+    return fail(FH_EINVAL, "fh_read_probe: need src, sink, bytes a multiple of 16 and 1..65536 blocks");
+  hipLaunchKernelGGL(read_probe_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), (const uint4*)src,
+                     (int64_t)(bytes / 16), sink);
+  return check_launch("fh_read_probe");
+}

@@ -63,6 +63,7 @@ SIGNATURES = {
   "fh_reduce": ([ctypes.POINTER(Program), I, I, L, L, L, P, I, P], I),
   "fh_argmax_rows": ([P, L, L, P, P], I),
   "fh_argmax_parts": ([P, L, L, P, P], I),
+  "fh_read_probe": ([P, S, P, I, P], I),
   "fh_heads_workspace_bytes": ([I, L, I], S),
   "fh_logit_heads": ([P, L, I, L, I, P, P, P, P, P, S, P], I),
 }

@@ -298,6 +298,12 @@ size_t fh_heads_workspace_bytes(int rows, int64_t vocab, int k);
 int fh_logit_heads(const float* logits, int64_t ldl, int rows, int64_t vocab, int k, const float* inv_temp,
                    float* values, int32_t* ids, float* lse, void* workspace, size_t ws_bytes, void* stream);
 
+/* ---- measurement ------------------------------------------------------------------------------------------
+ * The read floor a matmul's weight stream is measured against (bench.py's read_floor): `bytes` (a multiple of 16) of
+ * src read once by `blocks` workgroups of 256 threads, 16 bytes a load and four loads in flight a thread, each
+ * workgroup's xor of the 32-bit words it read into sink[block] ([blocks] uint32). No counterpart in the reference. */
+int fh_read_probe(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,7 +4,8 @@
 - an FH_EP_PROGRAM epilogue reads its per-row inputs at the call's row when the GEMV takes more rows than one launch
   does (rows 8 and up: several launches, each its own rows);
 - the Decoder refuses, on the host, a slot outside its cache and a step past its context (so no kernel is ever handed
-  a cache row outside the cache)."""
+  a cache row outside the cache);
+- fh_read_probe, the read floor bench.py measures the GEMVs against, reads every byte it is given."""
 import math
 import numpy as np
 import pytest
@@ -102,3 +103,19 @@ def test_decoder_refuses_rows_outside_its_cache(cuda):
   dec.advance()  # places 6 and 7: the last row of each slot
   with pytest.raises(ValueError, match="advance"):
     dec.advance()
+
+
+def test_read_probe_reads_every_byte(cuda):
+  # fh_read_probe (bench.py's read floor): the xor of the workgroups' sinks is the xor of every 32-bit word, so each
+  # byte was read, once or an odd number of times; sizes with a ragged tail past the four-load steps
+  from ferrite_amd import lib
+  rng = np.random.default_rng(71)
+  for words, blocks in ((4, 1), (4 * 1000 + 4, 7), (1 << 20, 2048), ((1 << 20) + 36, 2048)):
+    data = rng.integers(0, 1 << 32, words, dtype=np.uint32)
+    src = torch.from_numpy(data.view(np.int32)).cuda()
+    sink = torch.zeros(blocks, dtype=torch.int32, device="cuda")
+    lib.call("fh_read_probe", src.data_ptr(), 4 * words, sink.data_ptr(), blocks, torch.cuda.current_stream().cuda_stream)
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
+    assert got == np.bitwise_xor.reduce(data), (words, blocks)
+  with pytest.raises(ValueError):
+    lib.call("fh_read_probe", src.data_ptr(), 10, sink.data_ptr(), blocks, None)
