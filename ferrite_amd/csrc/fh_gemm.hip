@@ -109,6 +109,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
   // re-reads the last.
   const int last = (K - 1) / GM_BK * GM_BK;
   auto load = [&](int k0, uint4 (&xr)[XW], Half (&wm)[4], uint32_t& we) {
+    __builtin_amdgcn_sched_barrier(0);  // (issued here, not sunk below the step's arithmetic)
     k0 = min(k0, last);
     const int kx = min(k0 + 32 * ah, K - 32);
     const uint4* p = (const uint4*)((const char*)a.x + (xrow * a.ldx + kx) * (XBF16 ? 2 : 4));
@@ -118,6 +119,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
 #pragma unroll
     for (int r = 0; r < 4; ++r) wm[r] = *(const Half*)(mrun + (int64_t)(k + r) * RB);
     we = *(const uint32_t*)(erun + k);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   auto store = [&](int k0, int stage, const uint4 (&xr)[XW], const Half (&wm)[4], uint32_t we) {
