@@ -245,7 +245,13 @@ __global__ __launch_bounds__(skinny_threads(XBF16, MB)) void skinny_kernel(MatAr
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < SQ; ++i) sum += sk + tpr * i < sqn ? sq[i] : 0.f;
-    for (int i = SQ * tpr + sk; i < sqn; i += tpr) sum += sqp[i];  // (more runs than SQ tpr)
+    for (int i0 = SQ * tpr + sk; i0 < sqn; i0 += SQ * tpr) {  // (more runs than SQ tpr: SQ loads at a time, added in order)
+      float v[SQ];
+#pragma unroll
+      for (int i = 0; i < SQ; ++i) v[i] = i0 + tpr * i < sqn ? sqp[i0 + tpr * i] : 0.f;
+#pragma unroll
+      for (int i = 0; i < SQ; ++i) sum += v[i];
+    }
     for (int m = tpr >> 1; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
     if (sk == 0 && srow < 16 * MB) rs_s[srow] = (has_ssq && srow < M) ? 1.0f / sqrtf(sum / (float)K + a.eps) : 1.f;
   }
