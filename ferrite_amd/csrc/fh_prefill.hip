@@ -3,8 +3,8 @@
 // Attention (models/llama.py:129-142 for a chunk of T consecutive places p0 .. p0 + T - 1 of one sequence, whose
 // keys and values are already in the cache: its own rows and every earlier place of the slot). A workgroup of 4 waves
 // takes 128 query rows of one query head, a wave 32 of them, and walks the keys in tiles of 64 that its rows reach,
-// each tile's loads in flight during the previous tile's arithmetic (a 2048-token prompt's attention 250 -> 470
-// TFLOP/s on MI355X with them).
+// each tile's loads in flight during the previous tile's arithmetic and the tile stored into the second of two LDS
+// buffers after it, one barrier a tile (a 2048-token prompt's attention 250 -> ~450 TFLOP/s on MI355X with them).
 // The scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_bf16, keys down, queries across), so that a lane
 // holds one query's scores: its softmax statistics need no cross-lane work beyond the two halves of the wave. The
 // online softmax (a running max and sum, rescaling the partial output) follows flash attention; the output is
@@ -74,8 +74,8 @@ template <int HD, int CF>
 __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
   constexpr int KLD = HD + 8;        // K tile row in LDS (bf16): 16-byte aligned, banks spread
   constexpr int VLD = PA_BK + 8;     // V^T tile row (bf16)
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[PA_BK * KLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[HD * VLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks2[2][PA_BK * KLD];  // two buffers: a tile's arithmetic reads
+  __shared__ __attribute__((aligned(16))) uint16_t Vt2[2][HD * VLD];     // one while the next tile is stored in the other
 
   const int ntiles = (a.T + PA_BQ - 1) / PA_BQ;
   // the longest tiles first; the second half of the heads shortest first, so that the two workgroups a CU holds
@@ -131,11 +131,10 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
       for (int j = 0; j < 4; ++j) vraw[j] = cache_raw<HD, CF>(a, vrow + min(k0 + 4 * kq + j, last_key), 8 * dg);
     }
   };
-  load_tile(0);
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int64_t k0 = (int64_t)kt * PA_BK;
-    __syncthreads();  // the previous tile's readers are done
-    // K rows into LDS, bf16; V^T: a thread's 4 keys x 8 dimensions as 8 rows of 4 keys
+  // a tile's loads, as bf16, into buffer b: K rows; V^T, a thread's 4 keys x 8 dimensions as 8 rows of 4 keys
+  auto store_tile = [&](int b) {
+    uint16_t* Ks = Ks2[b];
+    uint16_t* Vt = Vt2[b];
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
       const int i = t + 256 * j, r = i / (HD / 8), c = (i % (HD / 8)) * 8;
@@ -157,7 +156,14 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
         *(uint2*)(Vt + (8 * dg + d) * VLD + 4 * kq) = make_uint2(k01, k23);
       }
     }
-    __syncthreads();
+  };
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int64_t k0 = (int64_t)kt * PA_BK;
+    const uint16_t* Ks = Ks2[kt & 1];
+    const uint16_t* Vt = Vt2[kt & 1];
     if (kt + 1 < nkt) load_tile(kt + 1);  // the next tile's loads in flight during this one's arithmetic
 
     // S^T for the tile's two blocks of 32 keys: block kb's value r of lane (ql, hh) is key 32 kb + 8 (r / 4) + 4 hh +
@@ -221,6 +227,8 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
           acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)&vv, pf, acc[d], 0, 0, 0);
         }
       }
+    if (kt + 1 < nkt) store_tile((kt + 1) & 1);  // (the other buffer: its last readers passed the previous barrier)
+    __syncthreads();
   }
 
   // o[row][h * HD + dim]: block d's value r of lane (ql, hh) is dimension 32 d + 8 (r / 4) + 4 hh + r % 4
