@@ -8,8 +8,10 @@
 // cores work on one stage, the threads' loads of the next step's x rows and weight rows are in flight, and once the
 // step's products are issued they convert them into the other stage: x to bf16 rows, the weight's 16-byte runs to bf16
 // columns (K-contiguous, as v_mfma_f32_32x32x16_bf16 takes its operands). One barrier a step. Each wave owns a 64 x 64
-// quarter, 2 x 2 blocks of 32 x 32, 16 MFMAs a step. The epilogue stages the tile in LDS as fp32 so that each output
-// sees its row's 1/rms and its pair partner, whichever wave computed it.
+// quarter, 2 x 2 blocks of 32 x 32, 16 MFMAs a step. Where the grid would not give every CU a workgroup anyway, a
+// workgroup of 8 waves takes 256 rows (4 x 2 waves of 64 x 64; the first 4 waves load and convert the weight, once for
+// all 256 rows). The epilogue stages the tile in LDS as fp32 so that each output sees its row's 1/rms and its pair
+// partner, whichever wave computed it.
 //
 // Tiles go to the XCDs in contiguous ranges (the hardware deals workgroups round-robin over the 8 XCDs) and within a
 // range in groups of 8 row tiles, so that an XCD's L2 keeps both the weight columns and the x rows it re-reads.
@@ -27,8 +29,6 @@ constexpr int GM_LD = GM_BK + 8;     // LDS row of a tile operand, bf16: 144 byt
 constexpr int GM_LDC = GM_BN + 4;    // LDS row of the fp32 output tile
 constexpr int GM_THREADS = 256;
 constexpr int GM_GROUP = 8;          // row tiles a group (tile order)
-constexpr int GM_STAGE = 2 * GM_BM * GM_LD * 2;  // one stage: x [128][72] and W [128][72], bf16: 36,864 bytes
-constexpr int GM_LDS = 2 * GM_STAGE;         // 73,728 bytes; the fp32 output tile [128][132] (67,584) aliases them
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
@@ -51,11 +51,15 @@ __device__ inline int64_t tile_run(const MatArgs& a, int tn, int lr) {
   return lr < 4 ? nb0 : nb0 + a.pair_half;
 }
 
-template <bool FOUR, bool XBF16, bool NORM>
-__global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tiles_m, int tiles_n, SkinnyMoe g) {
-  __shared__ __attribute__((aligned(16))) char smem[GM_LDS];
-  __shared__ float rs_s[GM_BM];
-  // stage s: x at smem + s * GM_STAGE ([128 rows][72] bf16), W after it ([128 columns][72] bf16, K-contiguous)
+template <bool FOUR, bool XBF16, bool NORM, int TM>  // TM: 128-row halves of the tile (1, or 2 with 8 waves)
+__global__ __launch_bounds__(GM_THREADS * TM, 3 - TM) void gemm_kernel(MatArgs a, int tiles_m, int tiles_n, SkinnyMoe g) {
+  constexpr int BM = GM_BM * TM, NT = GM_THREADS * TM;
+  constexpr int STAGE = (BM + GM_BN) * GM_LD * 2;
+  constexpr int LDS = 2 * STAGE > BM * GM_LDC * 4 ? 2 * STAGE : BM * GM_LDC * 4;
+  __shared__ __attribute__((aligned(16))) char smem[LDS];
+  __shared__ float rs_s[BM];
+  // stage s: x at smem + s * STAGE ([BM rows][72] bf16), W after it ([128 columns][72] bf16, K-contiguous); the fp32
+  // output tile [BM][132] aliases them after the K loop
   float* Cs = (float*)smem;                            // [128][132]: the output tile (after the K loop)
 
   // the rows of this matmul, its first output row, its weight (gathered: expert blockIdx.y's; `a` itself is left as
@@ -70,7 +74,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
     ybase = (int64_t)e * a.M;
     wmant += e * g.expert_mant;
     wexps += e * g.expert_exps;
-    tiles_m = (int)((M + GM_BM - 1) / GM_BM);
+    tiles_m = (int)((M + BM - 1) / BM);
     const int q = (tiles_m * tiles_n + 7) / 8;
     if (id >= 8 * q) return;
     id = (id % 8) * q + id / 8;
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
   const int first_m = id / per_group * GM_GROUP;
   const int gm = min(tiles_m - first_m, GM_GROUP);
   const int tm = first_m + (id % per_group) % gm, tn = (id % per_group) / gm;
-  const int64_t m0 = (int64_t)tm * GM_BM;
+  const int64_t m0 = (int64_t)tm * BM;
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int K = (int)a.K;
@@ -94,7 +98,8 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
   const int64_t xr0 = min(m0 + ar, M - 1);
   const int64_t xrow = g.counts ? (g.x_rows ? (int64_t)g.x_rows[ybase + xr0] : ybase + xr0) : xr0;
   const bool xok = m0 + ar < M;
-  const int lr = t >> 5, rq = (t & 31) >> 1, ch = t & 1;
+  const int lr = (t >> 5) & 7, rq = (t & 31) >> 1, ch = t & 1;
+  const bool wt = TM == 1 || t < GM_THREADS;  // (the weight's loads and conversion: the first 256 threads)
   const int64_t nb = tile_run(a, tn, lr);
   constexpr int RB = FOUR ? 8 : 16;
   const uint8_t* mrun = wmant + (nb < 0 ? 0 : nb) * a.K * RB + ch * (RB / 2);
@@ -116,15 +121,17 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
 #pragma unroll
     for (int i = 0; i < XW; ++i) xr[i] = p[i];
     const int k = min(k0 + 4 * rq, K - 4);  // (K is a multiple of 32)
+    if (wt) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) wm[r] = *(const Half*)(mrun + (int64_t)(k + r) * RB);
-    we = *(const uint32_t*)(erun + k);
+      for (int r = 0; r < 4; ++r) wm[r] = *(const Half*)(mrun + (int64_t)(k + r) * RB);
+      we = *(const uint32_t*)(erun + k);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 
   auto store = [&](int k0, int stage, const uint4 (&xr)[XW], const Half (&wm)[4], uint32_t we) {
-    uint16_t* As = (uint16_t*)(smem + stage * GM_STAGE);
-    uint16_t* Bs = As + GM_BM * GM_LD;
+    uint16_t* As = (uint16_t*)(smem + stage * STAGE);
+    uint16_t* Bs = As + BM * GM_LD;
     // x -> bf16 (times the RMSNorm weight), 4 x 16 bytes
     const int kx = min(k0 + 32 * ah, K - 32);
     if (XBF16 && !NORM) {
@@ -167,6 +174,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
     }
 
     // the weight's 4 rows x 8 columns -> 8 columns of 4 bf16 (one 8-byte LDS write each); rows past K are zero
+    if (!wt) return;
     float f[4][8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) magnitudes8(wm[r], f[r]);
@@ -210,8 +218,8 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
   const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
   const int fr = lane & 31, fk = 8 * (lane >> 5);
   auto compute = [&](int stage) {
-    const uint16_t* As = (const uint16_t*)(smem + stage * GM_STAGE);
-    const uint16_t* Bs = As + GM_BM * GM_LD;
+    const uint16_t* As = (const uint16_t*)(smem + stage * STAGE);
+    const uint16_t* Bs = As + BM * GM_LD;
 #pragma unroll
     for (int kk = 0; kk < GM_BK; kk += 16) {
       bf16x8 af[2], bfr[2];
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
     const int c = t & 127;
     const int64_t run = tile_run(a, tn, c >> 4);
     const int64_t col = run * 16 + (c & 15);
-    for (int r = t >> 7; r < GM_BM; r += 2) {
+    for (int r = t >> 7; r < BM; r += NT / 128) {
       const int64_t m = m0 + r;
       if (m < M && run >= 0)
         store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + col, prog_eval(a.prog, Cs[r * GM_LDC + c] * rs_s[r], 0, m, col));
@@ -266,7 +274,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
     const int c = t & 127, j = c & 15;
     const int64_t run = tile_run(a, tn, c >> 4);
     const int64_t col = run * 16 + j;
-    for (int r = t >> 7; r < GM_BM; r += 2) {
+    for (int r = t >> 7; r < BM; r += NT / 128) {
       const int64_t m = m0 + r;
       const bool ok = m < M && run >= 0;
       const int64_t at = (ybase + m) * a.ldy + col;
@@ -295,7 +303,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
     const int c = t & 63, p = c >> 4, j = c & 15;
     const int64_t run = tile_run(a, tn, p);
     const int64_t c0 = run * 16 + j;
-    for (int r = t >> 6; r < GM_BM; r += 4) {
+    for (int r = t >> 6; r < BM; r += NT / 64) {
       const int64_t m = m0 + r;
       if (m >= M || run < 0) continue;
       float x0 = Cs[r * GM_LDC + c] * rs_s[r], x1 = Cs[r * GM_LDC + c + 64] * rs_s[r];
@@ -326,25 +334,38 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_kernel(MatArgs a, int tile
 
 // The tiled kernel over a's M rows (per expert, gathered, when g.counts is set: grid.y = experts)
 int gemm_tiles(const MatArgs& a, const SkinnyMoe& g, int fmt, int experts, hipStream_t s) {
-  const int64_t tiles_m = (a.M + GM_BM - 1) / GM_BM;
-  const int64_t tiles_n = a.P == 1 ? (a.N / 16 + 7) / 8 : ((int64_t)a.items + 3) / 4;
+  // 256-row tiles (8 waves, the weight's conversion shared by twice the rows) where they still give every CU a
+  // workgroup or fewer (measured at 2048 rows of the 8B shapes: o 720 -> 765 TFLOP/s, down 780 -> 895; qkv and gate_up,
+  // with more tiles than CUs, slower), 128-row tiles (4 waves, two workgroups a CU) otherwise
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+    return n;
+  }();
+  const int64_t tiles_n0 = a.P == 1 ? (a.N / 16 + 7) / 8 : ((int64_t)a.items + 3) / 4;
+  const int TMv = (!g.counts && (a.M + 2 * GM_BM - 1) / (2 * GM_BM) * tiles_n0 <= cus) ? 2 : 1;
+  const int64_t tiles_m = (a.M + GM_BM * TMv - 1) / (GM_BM * TMv);
+  const int64_t tiles_n = tiles_n0;
   if (tiles_m * tiles_n >= (1LL << 31)) return fail(FH_EUNSUP, "fh_gemm_bfp: too many tiles");
   if (g.counts && (a.ssq_in || a.kind == FH_EP_ROPE_KV || a.kind == FH_EP_RESIDUAL)) return fail(FH_EUNSUP, "gathered GEMM: STORE or SILU_GATE, no prologue");
   // (gathered: a grid for the most rows an expert can have, in whole multiples of the 8 XCDs)
   const int64_t tiles = g.counts ? (tiles_m * tiles_n + 7) / 8 * 8 : tiles_m * tiles_n;
-  const dim3 grid((unsigned)tiles, g.counts ? experts : 1), b(GM_THREADS);
+  const dim3 grid((unsigned)tiles, g.counts ? experts : 1), b(GM_THREADS * TMv);
   const int tm = (int)tiles_m, tn = (int)tiles_n;
   const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
+#define GM_LAUNCH(F, X, N) do { if (TMv == 2) hipLaunchKernelGGL((gemm_kernel<F, X, N, 2>), grid, b, 0, s, a, tm, tn, g); \
+                                 else hipLaunchKernelGGL((gemm_kernel<F, X, N, 1>), grid, b, 0, s, a, tm, tn, g); } while (0)
   switch (which) {
-    case 0: hipLaunchKernelGGL((gemm_kernel<false, false, false>), grid, b, 0, s, a, tm, tn, g); break;
-    case 1: hipLaunchKernelGGL((gemm_kernel<false, false, true>), grid, b, 0, s, a, tm, tn, g); break;
-    case 2: hipLaunchKernelGGL((gemm_kernel<false, true, false>), grid, b, 0, s, a, tm, tn, g); break;
-    case 3: hipLaunchKernelGGL((gemm_kernel<false, true, true>), grid, b, 0, s, a, tm, tn, g); break;
-    case 4: hipLaunchKernelGGL((gemm_kernel<true, false, false>), grid, b, 0, s, a, tm, tn, g); break;
-    case 5: hipLaunchKernelGGL((gemm_kernel<true, false, true>), grid, b, 0, s, a, tm, tn, g); break;
-    case 6: hipLaunchKernelGGL((gemm_kernel<true, true, false>), grid, b, 0, s, a, tm, tn, g); break;
-    default: hipLaunchKernelGGL((gemm_kernel<true, true, true>), grid, b, 0, s, a, tm, tn, g); break;
+    case 0: GM_LAUNCH(false, false, false); break;
+    case 1: GM_LAUNCH(false, false, true); break;
+    case 2: GM_LAUNCH(false, true, false); break;
+    case 3: GM_LAUNCH(false, true, true); break;
+    case 4: GM_LAUNCH(true, false, false); break;
+    case 5: GM_LAUNCH(true, false, true); break;
+    case 6: GM_LAUNCH(true, true, false); break;
+    default: GM_LAUNCH(true, true, true); break;
   }
+#undef GM_LAUNCH
   return FH_OK;
 }
 
