@@ -43,3 +43,39 @@ def test_errors_without_gpu_work():
   assert kb(lib.F32, 2, 10, 64) == 4 * 10 * 64 * 4 and kb(lib.BF16, 2, 10, 64) == 4 * 10 * 64 * 2
   assert kb(lib.BFP8, 2, 10, 128) == 4 * 10 * (128 + 8) and kb(lib.BFP4, 2, 10, 128) == 4 * 10 * (64 + 8)
   assert kb(lib.BFP8, 2, 10, 48) == 0 and kb(7, 2, 10, 64) == 0
+
+
+def test_tile_layout_and_its_refusals():
+  # FH_BF16_T16: the header's value is the binding's, ops' helpers follow the layout's formula (element (r, c) at
+  # (r // 16) 16 ld + (c // 8) 128 + (r % 16) 8 + c % 8, whole tiles of 16 rows), and the entry points refuse on the
+  # host, before any launch, what the layout does not cover
+  import torch
+  from ferrite_amd import ops
+  assert re.search(r"#define FH_BF16_T16 (\d+)", HEADER.read_text()).group(1) == str(lib.BF16_T16)
+  x = (torch.arange(37 * 24, dtype=torch.float32) % 251).view(37, 24)
+  t = ops.to_tiles16(x, fill=-1.0)
+  flat = t.data.float()
+  assert flat.numel() == 48 * 24
+  for r in range(37):
+    for c in range(24):
+      assert flat[(r // 16) * 16 * 24 + (c // 8) * 128 + (r % 16) * 8 + c % 8] == (r * 24 + c) % 251
+  assert (flat[2 * 16 * 24:].view(3, 16, 8)[:, 5:, :] == -1).all()  # (rows 37..47 of the last tile: the fill)
+  assert torch.equal(t.rows_(), x.to(torch.bfloat16))
+  with pytest.raises(ValueError):
+    ops.tiles16(3, 12)  # (columns a multiple of 8)
+  if not lib.PATH.exists(): pytest.skip("libferrite_hip.so not built")
+  lib.load()
+  buf = ctypes.create_string_buffer(1 << 16)
+  p = ctypes.addressof(buf)
+  # more than 64 rows: the tiled GEMM takes rows only
+  with pytest.raises(NotImplementedError, match="FH_BF16_T16"):
+    lib.call("fh_gemm_bfp", p, lib.BF16_T16, 64, 65, 64, 16, p, p, lib.BFP8, None, p, lib.F32, 16, None)
+  with pytest.raises(NotImplementedError, match="FH_BF16_T16"):
+    lib.call("fh_gemm_bfp", p, lib.BF16, 64, 65, 64, 16, p, p, lib.BFP8, None, p, lib.BF16_T16, 16, None)
+  # the GEMV writes rows only; fh_rms_rows' tiles need whole groups of 8 columns; the read probe whole 16 bytes
+  with pytest.raises(ValueError):
+    lib.call("fh_gemv_bfp", p, lib.F32, 64, 1, 64, 16, p, p, lib.BFP8, None, p, lib.BF16_T16, 16, None)
+  with pytest.raises(ValueError, match="multiple of 8"):
+    lib.call("fh_rms_rows", p, 12, 2, 12, p, ctypes.c_float(1e-5), 0, p, lib.BF16_T16, 12, None)
+  with pytest.raises(ValueError):
+    lib.call("fh_read_probe", p, 10, p, 1, None)
