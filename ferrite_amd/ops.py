@@ -108,7 +108,7 @@ class Tiles16:
   @property
   def dtype(self): return "bf16_t16"
 
-  def rows_(self):
+  def to_rows(self):
     """The rows as a [rows][cols] bf16 tensor (a copy)."""
     r16 = -(-self.rows // 16) * 16
     t = self.data.view(r16 // 16, self.cols // 8, 16, 8).permute(0, 2, 1, 3).reshape(r16, self.cols)

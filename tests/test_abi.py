@@ -60,7 +60,7 @@ def test_tile_layout_and_its_refusals():
     for c in range(24):
       assert flat[(r // 16) * 16 * 24 + (c // 8) * 128 + (r % 16) * 8 + c % 8] == (r * 24 + c) % 251
   assert (flat[2 * 16 * 24:].view(3, 16, 8)[:, 5:, :] == -1).all()  # (rows 37..47 of the last tile: the fill)
-  assert torch.equal(t.rows_(), x.to(torch.bfloat16))
+  assert torch.equal(t.to_rows(), x.to(torch.bfloat16))
   with pytest.raises(ValueError):
     ops.tiles16(3, 12)  # (columns a multiple of 8)
   if not lib.PATH.exists(): pytest.skip("libferrite_hip.so not built")

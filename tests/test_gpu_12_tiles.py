@@ -38,7 +38,7 @@ def test_tile_layout_helpers(cuda):
     for c in (0, 7, 8, 23):
       assert flat[(r // 16) * 16 * 24 + (c // 8) * 128 + (r % 16) * 8 + c % 8] == (r * 24 + c) % 251
   assert t.data.numel() == 48 * 24
-  same(t.rows_(), x.to(torch.bfloat16), "rows_ inverts to_tiles16")
+  same(t.to_rows(), x.to(torch.bfloat16), "to_rows inverts to_tiles16")
 
 
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
@@ -64,12 +64,12 @@ def test_matmul_tiles_equal_rows(cuda, fmt):
     # STORE into bf16 tiles
     yt = ops().tiles16(M, N, fill=float("nan"))
     ops().gemm(xt, bw, out=yt)
-    same(yt.rows_(), ops().gemm(x, bw, out_dtype=torch.bfloat16), ("STORE bf16 tiles", M))
+    same(yt.to_rows(), ops().gemm(x, bw, out_dtype=torch.bfloat16), ("STORE bf16 tiles", M))
     # SiLU * gate into bf16 tiles (down's x in a decode step)
     ep = lambda: ops().epilogue(L.EP_SILU_GATE, split=N // 2)
     ht = ops().tiles16(M, N // 2)
     ops().gemm(xt, bw, ep(), out=ht)
-    same(ht.rows_(), ops().gemm(x, bw, ep(), out_dtype=torch.bfloat16), ("SILU_GATE tiles", M))
+    same(ht.to_rows(), ops().gemm(x, bw, ep(), out_dtype=torch.bfloat16), ("SILU_GATE tiles", M))
     # the residual epilogue's bf16 copy (times the next norm's weight) in tiles
     res = torch.from_numpy(rng.normal(0, 1, (M, N)).astype(np.float32)).cuda()
     cw = torch.from_numpy(rng.normal(1, 0.1, N).astype(np.float32)).cuda()
@@ -81,7 +81,7 @@ def test_matmul_tiles_equal_rows(cuda, fmt):
     ops().gemm(xt, bw, ops().epilogue(L.EP_RESIDUAL, residual=y2, ssq_out=s2, copy_bf16=c_tiles, copy_w=cw), out=y2)
     same(y2, y1, ("RESIDUAL y", M))
     same(s2, s1, ("RESIDUAL ssq", M))
-    same(c_tiles.rows_(), c_rows, ("RESIDUAL copy tiles", M))
+    same(c_tiles.to_rows(), c_rows, ("RESIDUAL copy tiles", M))
 
 
 def test_gemv_copy_tiles(cuda):
@@ -99,7 +99,7 @@ def test_gemv_copy_tiles(cuda):
   ops().gemv(x, bw, ops().epilogue(L.EP_RESIDUAL, residual=y1, copy_bf16=c_rows), out=y1)
   ops().gemv(x, bw, ops().epilogue(L.EP_RESIDUAL, residual=y2, copy_bf16=c_tiles), out=y2)
   same(y2, y1, "GEMV y")
-  same(c_tiles.rows_(), c_rows, "GEMV copy tiles")
+  same(c_tiles.to_rows(), c_rows, "GEMV copy tiles")
 
 
 def test_attention_and_rms_tiles(cuda):
@@ -116,13 +116,13 @@ def test_attention_and_rms_tiles(cuda):
     o_tiles = ops().tiles16(B, heads * hd, fill=float("nan"))
     ops().attention_decode(q, cache, heads, kv, hd, pl, first, context, ws, o=o_rows)
     ops().attention_decode(q, cache, heads, kv, hd, pl, first, context, ws, o=o_tiles)
-    same(o_tiles.rows_(), o_rows, ("attention o tiles", context))
+    same(o_tiles.to_rows(), o_rows, ("attention o tiles", context))
   x = torch.from_numpy(rng.normal(0, 1, (B, 4096)).astype(np.float32)).cuda()
   g = torch.from_numpy(rng.normal(1, 0.1, 4096).astype(np.float32)).cuda()
   r_rows = ops().rms_rows(x, g, 1e-5)
   r_tiles = ops().tiles16(B, 4096, fill=float("nan"))
   ops().rms_rows(x, g, 1e-5, out=r_tiles)
-  same(r_tiles.rows_(), r_rows, "rms_rows tiles")
+  same(r_tiles.to_rows(), r_rows, "rms_rows tiles")
 
 
 def test_tiles_refused_past_64_rows(cuda):
