@@ -192,6 +192,29 @@ def gemm(x, bw, ep=None, out=None, out_dtype=torch.float32):
   return _matmul("fh_gemm_bfp", x, bw, ep, out, out_dtype)
 
 
+_DT_OUT = {torch.float32: lib.F32, torch.bfloat16: lib.BF16, torch.int32: lib.I32}
+
+
+def matmul(a, b, program=None, out=None, out_dtype=torch.float32):
+  """out[i] = program(a[i] @ b[i]) (fh_matmul) for plain operands: a [batch][M][K], b [batch][K][N] (fp32 or bf16,
+  rows contiguous; a batch of 1 serves every entry), out [batch][M][N] (fp32, bf16 or int32, rows contiguous). An fp32
+  operand goes in as ferrite's bf16x3. program: an fh_program over the sum (lib.OPND_ACC), or None to store it."""
+  _dev(a, b)
+  if a.dim() != 3 or b.dim() != 3 or a.shape[2] != b.shape[1]: raise ValueError(f"matmul: {tuple(a.shape)} @ {tuple(b.shape)}")
+  if a.dtype not in _TORCH or b.dtype not in _TORCH: raise ValueError("matmul: fp32 or bf16 operands")
+  if a.stride(2) != 1 or b.stride(2) != 1: raise ValueError("matmul: operands' rows contiguous")
+  batch = max(a.shape[0], b.shape[0])
+  if a.shape[0] not in (1, batch) or b.shape[0] not in (1, batch): raise ValueError(f"matmul: batches {a.shape[0]} and {b.shape[0]}")
+  M, K, N = a.shape[1], a.shape[2], b.shape[2]
+  if out is None: out = torch.empty(batch, M, N, dtype=out_dtype, device=a.device)
+  if tuple(out.shape) != (batch, M, N) or out.stride(2) != 1 or out.dtype not in _DT_OUT: raise ValueError(f"matmul: out {tuple(out.shape)}")
+  sa = a.stride(0) if a.shape[0] > 1 else 0
+  sb = b.stride(0) if b.shape[0] > 1 else 0
+  lib.call("fh_matmul", _ptr(a), _TORCH[a.dtype], sa, a.stride(1), _ptr(b), _TORCH[b.dtype], sb, b.stride(1), batch, M, K, N,
+           ctypes.byref(program) if program is not None else None, _ptr(out), _DT_OUT[out.dtype], out.stride(0), out.stride(1), _stream())
+  return out
+
+
 def embed_rows(table, ids, x=None, ssq=None):
   """Rows ids of table into x (fp32), with their sums of squares by runs of 16 (fh_embed_rows)."""
   _dev(table, ids)

@@ -335,7 +335,10 @@ class Tensor:
 
   def matmul(self, x, dtype=None, fidelity=None, index=None):
     """self (1 x rows x K) @ x (K x N, a block float: bfp8 or bfp4, cast once), written as dtype: bf16, or fp32 if
-    self is, unless said. fp32 rows, a few, go through the exact-product GEMV; otherwise the matrix cores take self's
+    self is, unless said. A plain x (bf16 or fp32, a batch of matrices or one; self's batch the same or 1): fh_matmul,
+    bf16 products summed in fp32, an fp32 operand as ferrite's bf16x3 (hi@hi + hi@lo + lo@hi), written as dtype: fp32
+    if either operand is, else bf16, unless said. fp32 rows, a few, by a block float go through the exact-product
+    GEMV; otherwise the matrix cores take self's
     values in bf16, as ferrite's chip does (bf16 rows: exact products too); the elementwise ops on top of it run in
     the same kernel. fidelity: the chip's product phases (ferrite/tensor.py:443-452); taken and ignored, the products
     here being exact or bf16 x bf16 whatever it says. index: an int32 (rows, k) tensor choosing, for each batch entry b
@@ -343,7 +346,12 @@ class Tensor:
     its only one), index's (b // k, b % k); an entry choosing none (x.batch or more) is zeros. It is resolved on the GPU
     (each matrix's product, then each entry's pick), so a recording replays it; ops.moe_experts is the path that reads
     only the chosen experts."""
-    if x.dtype not in BFP: raise NotImplementedError("matmul: B is a block float (bfp8 or bfp4) on this runtime")
+    if x.dtype not in BFP:  # plain operands (fh_matmul): bf16 products summed in fp32, an fp32 operand as bf16x3
+      assert index is None, "index= picks among a batch of block floats"
+      assert "int32" not in (self.dtype, x.dtype), "the matrix cores multiply floats"
+      assert self.cols == x.rows and (self.batch == x.batch or 1 in (self.batch, x.batch)), f"{self.shape} @ {x.shape}"
+      dtype = dtype or ("fp32" if "fp32" in (self.dtype, x.dtype) else "bf16")
+      return Tensor(self.rt, self.rows, x.cols, "matmul", (self, x), max(self.batch, x.batch), dtype)
     if index is not None:
       assert index.dtype == "int32" and self.cols == x.rows and self.batch in (1, index.rows * index.cols) and index.batch == 1, \
         f"{self.shape} @ {x.shape} picked by {index.shape} {index.dtype}"
@@ -384,7 +392,12 @@ class Tensor:
     mm = next((t for t in _walk(self) if getattr(t, "_acc", False)), None)
     with self.rt.on(): out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
     p = _cprogram(prog, inputs)
-    if mm is not None:
+    if mm is not None and mm.srcs[1].dtype not in BFP:  # plain operands: every batch entry, rows contiguous
+      mm._acc = False
+      a, b = (u.realize() for u in mm.srcs)
+      a, b = ((u if u.data.stride(2) == 1 else (u + 0).realize()) for u in (a, b))
+      self.rt.run(lambda: ops.matmul(a.data, b.data, p, out=out), "matmul")
+    elif mm is not None:
       mm._acc = False
       a, w = mm.srcs[0].realize(), mm.srcs[1].data
       if a.data.stride(2) != 1: a = (a + 0).realize()  # rows contiguous (our copy kernel)

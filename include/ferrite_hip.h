@@ -270,6 +270,15 @@ int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim, const flo
 int fh_map(const fh_program* program, void* out, int out_dtype, int64_t batch, int64_t rows, int64_t cols, int64_t ldb,
            int64_t ldo, void* stream);
 
+/* C[b] = program(A[b] @ B[b]) for plain operands (Tensor.matmul with a bf16 or fp32 B, ferrite/tensor.py:443-485):
+ * A [M][K] rows lda apart, B [K][N] rows ldb apart, each FH_BF16 or FH_F32, batches a_batch_stride / b_batch_stride
+ * elements apart (0: one matrix for every batch entry); C [M][N] rows ldc apart, FH_F32, FH_BF16 (nearest even) or
+ * FH_I32. bf16 products summed in fp32; an FH_F32 operand as ferrite's bf16x3 (hi@hi + hi@lo + lo@hi, tensor.py:674-689).
+ * program: the elementwise ops on the sum (FH_OPND_ACC), evaluated at (b, row, col); NULL stores the sum. */
+int fh_matmul(const void* a, int a_dtype, int64_t a_batch_stride, int64_t lda, const void* b, int b_dtype,
+              int64_t b_batch_stride, int64_t ldb, int64_t batch, int64_t M, int64_t K, int64_t N,
+              const fh_program* program, void* c, int c_dtype, int64_t c_batch_stride, int64_t ldc, void* stream);
+
 /* The program's values summed (FH_REDUCE_SUM) or their largest (FH_REDUCE_MAX) along an axis of (batch, rows, cols)
  * (0, 1 or 2), out holding the result with that axis 1 (ferrite/tensor.py's _reduce, 362-368; FOLDS and COMBINE,
  * ferrite/compiler.py:345-348). fp32 sums in a fixed order. */
