@@ -273,3 +273,29 @@ extern "C" int fh_logit_heads(const float* logits, int64_t ldl, int rows, int64_
   if (parts > 1) hipLaunchKernelGGL(heads_merge, dim3(rows), dim3(HT), 0, s, a);
   return check_launch("fh_logit_heads");
 }
+
+namespace fh {
+
+// out[r][j] = src[r][idx[r][j]] for 4-byte elements, an index outside [0, cols) read at the nearest column
+__global__ __launch_bounds__(256) void gather_cols_kernel(const uint32_t* src, int64_t lds, int64_t cols, const int32_t* idx,
+                                                          int64_t ldi, int64_t rows, int64_t k, uint32_t* out, int64_t ldo) {
+  const int64_t n = rows * k;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / k, j = i % k;
+    int64_t c = idx[r * ldi + j];
+    c = c < 0 ? 0 : (c >= cols ? cols - 1 : c);
+    out[r * ldo + j] = src[r * lds + c];
+  }
+}
+
+}  // namespace fh
+
+extern "C" int fh_gather_cols(const void* src, int64_t lds, int64_t cols, const int32_t* idx, int64_t ldi, int64_t rows,
+                              int64_t k, void* out, int64_t ldo, void* stream) {
+  if (!src || !idx || !out) return fail(FH_EINVAL, "fh_gather_cols: null pointer");
+  if (rows < 1 || k < 1 || cols < 1 || lds < cols || ldi < k || ldo < k) return fail(FH_EINVAL, "fh_gather_cols: bad sizes");
+  const int64_t blocks = (rows * k + 255) / 256;
+  hipLaunchKernelGGL(gather_cols_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256), 0, as_stream(stream),
+                     (const uint32_t*)src, lds, cols, idx, ldi, rows, k, (uint32_t*)out, ldo);
+  return check_launch("fh_gather_cols");
+}

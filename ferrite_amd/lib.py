@@ -67,6 +67,7 @@ SIGNATURES = {
   "fh_read_probe": ([P, S, P, I, P], I),
   "fh_heads_workspace_bytes": ([I, L, I], S),
   "fh_logit_heads": ([P, L, I, L, I, P, P, P, P, P, S, P], I),
+  "fh_gather_cols": ([P, L, L, P, L, L, L, P, L, P], I),
 }
 
 _lib = None

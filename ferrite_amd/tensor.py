@@ -313,22 +313,52 @@ class Tensor:
 
   def topk(self, k, parts=1, labels=None):
     """Each row's k (<= 64) largest values, largest first, and their columns (int32), the first column of equal values
-    first (Tensor.topk, ferrite/tensor.py:373-388: numpy's stable order), by fh_logit_heads. ferrite's parts and labels
-    split a row too wide for a worker's L1 into two topk calls; one call here takes a whole row (parts 1, no labels)."""
-    if parts != 1 or labels is not None: raise NotImplementedError("topk: one call selects over a whole row (parts=1, labels=None)")
-    assert self.dtype in ("bf16", "fp32") and 1 <= k <= min(self.cols, 64), "bf16 or fp32, k of at most 64"
-    n, cols = self.batch * self.rows, self.cols
-    ld = (cols + 3) // 4 * 4  # rows 16-byte aligned for the kernel's loads
-    with self.rt.on(): x = torch.empty(n, ld, dtype=torch.float32, device=self.rt.device)
+    first (Tensor.topk, ferrite/tensor.py:373-388: numpy's stable order), by fh_logit_heads. parts: each row cut into
+    so many parts of equal width, each part's k best side by side, (rows, parts k), each index its column in the whole
+    row. labels: an int32 tensor of this one's shape (parts 1), each pick's label (labels at its column) instead of its
+    column: a second topk over the parts' best given their indices picks the whole row's best with its columns. One call
+    here takes a row of any width; parts and labels keep ferrite's two-call form working."""
+    assert self.dtype in ("bf16", "fp32"), "bf16 or fp32"
+    cols = self.cols // parts
+    assert 1 <= k <= min(cols, 64) and parts * cols == self.cols, "k of at most 64 and the row's width, whole parts"
+    assert labels is None or (labels.dtype == "int32" and labels.shape == self.shape and parts == 1), "labels: int32, x's shape"
+    n = self.batch * self.rows
+    R, ld = n * parts, (cols + 3) // 4 * 4  # each part a row of its own, rows 16-byte aligned for the kernel's loads
+    with self.rt.on(): x = torch.empty(R, ld, dtype=torch.float32, device=self.rt.device)
     prog, inputs = _fit_program(self.float() if self.dtype != "fp32" else self, self.shape, allow_acc=False)
     p = _cprogram(prog, inputs)
-    self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(x), lib.F32, *self.shape, self.rows * ld, ld, ops._stream()), "map")
+    if ld == cols:  # the parts of a row are consecutive rows of width cols: the row as it is
+      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(x), lib.F32, *self.shape, self.rows * self.cols,
+                                   self.cols, ops._stream()), "map")
+    else:  # the rows first, then each part into a row of its own, padded
+      with self.rt.on(): x0 = torch.empty(n, self.cols, dtype=torch.float32, device=self.rt.device)
+      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(x0), lib.F32, *self.shape, self.rows * self.cols,
+                                   self.cols, ops._stream()), "map")
+      q = lib.Program()
+      q.n_ops, q.n_inputs = 1, 1
+      q.op[0], q.a[0], q.b[0] = lib.OP["copy"], 16, lib.OPND_IMM
+      q.input[0], q.in_dtype[0] = x0.data_ptr(), lib.F32
+      q.in_stride[0][0], q.in_stride[0][1], q.in_stride[0][2] = 0, cols, 1
+      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(q), ops._ptr(x), lib.F32, 1, R, cols, R * ld, ld, ops._stream()), "map")
     values, ids = self.rt.run(lambda: ops.logit_heads(x[:, :cols], k), "topk")
-    v = Tensor(self.rt, self.rows, k, batch=self.batch, dtype="fp32")
-    v.data = values.reshape(self.batch, self.rows, k)
-    i = Tensor(self.rt, self.rows, k, batch=self.batch, dtype="int32")
-    i.data = ids.reshape(self.batch, self.rows, k)
-    return (v if self.dtype == "fp32" else v.cast(self.dtype)), i
+    i = Tensor(self.rt, R, k, dtype="int32")
+    i.data = ids.reshape(1, R, k)
+    if parts > 1:  # each part's columns from its first in the whole row
+      first = Tensor.of(self.rt, [[(r % parts) * cols] for r in range(R)], "int32")
+      i = (i + first).realize()
+    if labels is not None:
+      lab = labels.realize()
+      if not lab.data.is_contiguous(): lab = (lab + 0).realize()
+      with self.rt.on(): got = torch.empty(n, k, dtype=torch.int32, device=self.rt.device)
+      self.rt.run(lambda: lib.call("fh_gather_cols", ops._ptr(lab.data), self.cols, self.cols, ops._ptr(i.data), k, n, k,
+                                   ops._ptr(got), k, ops._stream()), "labels")
+      i = Tensor(self.rt, R, k, dtype="int32")
+      i.data = got.reshape(1, R, k)
+    v = Tensor(self.rt, self.rows, parts * k, batch=self.batch, dtype="fp32")
+    v.data = values.reshape(self.batch, self.rows, parts * k)
+    ids_out = Tensor(self.rt, self.rows, parts * k, batch=self.batch, dtype="int32")
+    ids_out.data = i.data.reshape(self.batch, self.rows, parts * k)
+    return (v if self.dtype == "fp32" else v.cast(self.dtype)), ids_out
 
   # ---- matmul (ferrite/tensor.py:443-485) ----------------------------------------------------------------------------
   def __matmul__(self, x): return self.matmul(x)

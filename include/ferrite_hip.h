@@ -307,6 +307,12 @@ size_t fh_heads_workspace_bytes(int rows, int64_t vocab, int k);
 int fh_logit_heads(const float* logits, int64_t ldl, int rows, int64_t vocab, int k, const float* inv_temp,
                    float* values, int32_t* ids, float* lse, void* workspace, size_t ws_bytes, void* stream);
 
+/* out[r][j] = src[r][idx[r][j]] (4-byte elements: int32 or fp32; rows lds, ldi, ldo apart), an index outside
+ * [0, cols) read at the nearest column: Tensor.topk's labels, each pick's label instead of its column
+ * (ferrite/tensor.py:373-388, topk_kernel's labels, compiler.py:1716-1838). */
+int fh_gather_cols(const void* src, int64_t lds, int64_t cols, const int32_t* idx, int64_t ldi, int64_t rows, int64_t k,
+                   void* out, int64_t ldo, void* stream);
+
 /* ---- measurement ------------------------------------------------------------------------------------------
  * The read floor a matmul's weight stream is measured against (bench.py's read_floor): `bytes` (a multiple of 16) of
  * src read once by `blocks` workgroups of 256 threads, 16 bytes a load and four loads in flight a thread, each

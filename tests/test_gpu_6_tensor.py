@@ -239,3 +239,37 @@ def test_topk(rt):
     want = np.argsort(-a, -1, kind="stable")[..., :20]
     assert np.array_equal(ids, want), dtype
     assert np.array_equal(np.array(v.tolist()), np.take_along_axis(a, want, -1))
+
+
+def test_topk_parts_and_labels(rt):
+  # ferrite's two-call form for rows wider than a worker's L1 (tensor.py:373-388): each part's k best side by side with
+  # their columns in the whole row, then a topk over those given the columns as labels gives the whole row's k best
+  # and their columns, ties in column order. Widths whose parts are not a multiple of 4 wide, and a batch.
+  rng = np.random.default_rng(69)
+  for parts, width in ((4, 1024), (3, 303), (5, 250)):
+    a = np.round(rng.normal(0, 2, (2, 3, width)) * 2) / 2
+    cols = width // parts
+    for dtype in ("bf16", "fp32"):
+      t = Tn().of(rt, a.tolist(), dtype)
+      v, i = t.topk(8, parts=parts)
+      assert v.dtype == dtype and i.dtype == "int32" and v.shape == i.shape == (2, 3, 8 * parts)
+      ids = np.array(i.tolist())
+      want = np.concatenate([np.argsort(-a[..., p * cols:(p + 1) * cols], -1, kind="stable")[..., :8] + p * cols for p in range(parts)], -1)
+      assert np.array_equal(ids, want), (parts, width, dtype)
+      assert np.array_equal(np.array(v.tolist()), np.take_along_axis(a, want, -1))
+      v2, i2 = v.topk(8, labels=i)
+      got = np.array(i2.tolist())
+      whole = np.argsort(-a, -1, kind="stable")[..., :8]
+      assert np.array_equal(got, whole), (parts, width, dtype)
+      assert np.array_equal(np.array(v2.tolist()), np.take_along_axis(a, whole, -1))
+  # the reference's own cases (test_sim.py:1492-1503): fp32 rows, k of 64 and 32, a tie across parts
+  for rows, cols, parts, k in ((5, 2560, 4, 64), (40, 1024, 2, 32)):
+    x = rng.normal(0, 3, (rows, cols)).astype(np.float32)
+    x[0, 100] = x[0, cols // 2 + 3] = x[0].max() + 1
+    values, ids = Tn().frombytes(rt, rows, cols, x.tobytes(), dtype="fp32").topk(k, parts)
+    w = cols // parts
+    want = np.concatenate([np.argsort(-x[:, p * w:(p + 1) * w], -1, kind="stable")[:, :k] + p * w for p in range(parts)], 1)
+    assert np.array_equal(np.array(ids.tolist()), want) and np.array_equal(np.array(values.tolist()), np.take_along_axis(x, want, -1))
+    values, ids = values.topk(k, labels=ids)
+    want = np.argsort(-x, -1, kind="stable")[:, :k]
+    assert np.array_equal(np.array(ids.tolist()), want) and np.array_equal(np.array(values.tolist()), np.take_along_axis(x, want, -1))
