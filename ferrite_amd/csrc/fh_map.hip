@@ -53,6 +53,37 @@ __global__ __launch_bounds__(256) void reduce_lines_kernel(fh_program p, int kin
   }
 }
 
+// a workgroup's fold of one value a thread, waves in order
+__device__ inline float block_fold256(int kind, float v, float* part) {
+  v = kind == FH_REDUCE_MAX ? wave_max(v) : wave_sum(v);
+  __syncthreads();  // (part is reused)
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = part[0];
+  for (int w = 1; w < 4; ++w) t = fold(kind, t, part[w]);
+  return t;
+}
+
+// softmax (or log_softmax) along each row of the program's values: a workgroup a (batch, row), three passes over the
+// row (its largest, the sum of exp(x - largest), the outputs), the program evaluated again each pass
+__global__ __launch_bounds__(256) void softmax_rows_kernel(fh_program p, int log_form, int64_t rows, int64_t cols, void* out,
+                                                           int out_dtype) {
+  __shared__ float part[4];
+  const int64_t r = blockIdx.x, b = blockIdx.y;
+  float m = -INFINITY;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) m = fmaxf(m, prog_eval(p, 0.f, b, r, c));
+  m = block_fold256(FH_REDUCE_MAX, m, part);
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) s += expf(prog_eval(p, 0.f, b, r, c) - m);
+  s = block_fold256(FH_REDUCE_SUM, s, part);
+  if (out_dtype == FH_BF16) s = bf16_to_f(bf16_rne_f(s));  // (the composed form's sum is a tensor of the rows' dtype)
+  const float ls = logf(s);
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float d = prog_eval(p, 0.f, b, r, c) - m;
+    prog_store(out, out_dtype, (b * rows + r) * cols + c, log_form ? d - ls : expf(d) / s);
+  }
+}
+
 static unsigned grid_for(int64_t n) {
   const int64_t g = (n + 255) / 256;
   return (unsigned)(g < 1 ? 1 : (g > 65536 ? 65536 : g));
@@ -88,4 +119,15 @@ extern "C" int fh_reduce(const fh_program* program, int kind, int axis, int64_t 
     hipLaunchKernelGGL(reduce_lines_kernel, dim3(grid_for(n)), dim3(256), 0, s, *program, kind, axis, batch, rows, cols, out, out_dtype);
   }
   return check_launch("fh_reduce");
+}
+
+extern "C" int fh_softmax_rows(const fh_program* program, int log_form, int64_t batch, int64_t rows, int64_t cols, void* out,
+                               int out_dtype, void* stream) {
+  if (int rc = check_program("fh_softmax_rows", program, false)) return rc;
+  if (!out || batch < 1 || rows < 1 || cols < 1) return fail(FH_EINVAL, "fh_softmax_rows: bad shape");
+  if (out_dtype != FH_F32 && out_dtype != FH_BF16) return fail(FH_EINVAL, "fh_softmax_rows: out is FH_F32 or FH_BF16");
+  if (rows > 0x7FFFFFFF || batch > 65535) return fail(FH_EUNSUP, "fh_softmax_rows: too many rows");
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows, (unsigned)batch), dim3(256), 0, as_stream(stream), *program,
+                     log_form, rows, cols, out, out_dtype);
+  return check_launch("fh_softmax_rows");
 }

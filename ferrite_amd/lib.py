@@ -62,6 +62,7 @@ SIGNATURES = {
   "fh_moe_experts": ([P, L, I, L, P, P, ctypes.c_float, I, I, L, P, P, I, P, P, I, P, P, P, P, P, S, P], I),
   "fh_map": ([ctypes.POINTER(Program), P, I, L, L, L, L, L, P], I),
   "fh_reduce": ([ctypes.POINTER(Program), I, I, L, L, L, P, I, P], I),
+  "fh_softmax_rows": ([ctypes.POINTER(Program), I, L, L, L, P, I, P], I),
   "fh_argmax_rows": ([P, L, L, P, P], I),
   "fh_argmax_parts": ([P, L, L, P, P], I),
   "fh_read_probe": ([P, S, P, I, P], I),

@@ -29,6 +29,7 @@ UNARY = ("relu", "exp", "exp2", "log", "log2", "sin", "cos", "recip", "sqrt", "f
 BINARY = ("add", "sub", "mul", "max", "cmplt", "cmpne", "keep", "drop")
 INT32_OPS = ("add", "sub", "max", "cmplt", "cmpne", "keep", "drop")
 REDUCE = {f"{f}{ax}": (f, ax) for f in ("sum", "max") for ax in range(3)}
+ROWWISE = ("softmax", "log_softmax")  # along each row, a launch of their own (fh_softmax_rows)
 
 
 class Runtime:
@@ -300,12 +301,20 @@ class Tensor:
     return s * (math.prod(s.shape) / math.prod(self.shape))
 
   def softmax(self, axis=-1):  # the max first, so exp stays in range
+    if axis % 3 == 2 and self.dtype != "int32": return self._rowwise("softmax")
     e = (self - self.max(axis)).exp()
     return e / e.sum(axis)
 
   def log_softmax(self, axis=-1):
+    if axis % 3 == 2 and self.dtype != "int32": return self._rowwise("log_softmax")
     m = self - self.max(axis)
     return m - m.exp().sum(axis).log()
+
+  def _rowwise(self, op):
+    """softmax / log_softmax along each row as one node: the same arithmetic as the composed form above (the row's
+    max, exp(x - max), its sum, the quotient or the difference of logs), one launch (fh_softmax_rows) that evaluates
+    the elementwise tree under it three times instead of two reductions and a map over realized rows."""
+    return Tensor(self.rt, self.rows, self.cols, op, (self,), self.batch, self.dtype)
 
   def layernorm(self, axis=-1, eps=1e-5):
     c = self - self.mean(axis)
@@ -407,6 +416,15 @@ class Tensor:
     if self.data is not None: return self
     if self.op == "picked":
       self._done(_picked(self).data)
+      return self
+    if self.op in ROWWISE:
+      src = self.srcs[0]
+      prog, inputs = _fit_program(src, src.shape, allow_acc=False)
+      with self.rt.on(): out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
+      p = _cprogram(prog, inputs)
+      self.rt.run(lambda: lib.call("fh_softmax_rows", ctypes.byref(p), int(self.op == "log_softmax"), *src.shape, ops._ptr(out),
+                                   DT[self.dtype], ops._stream()), "softmax")
+      self._done(out)
       return self
     if self.op in REDUCE:
       f, axis = REDUCE[self.op]
@@ -535,7 +553,7 @@ def _ops(t, acc_ok):
   """How many program ops t's tree would take, counting each shared node once and stopping at what realizes apart."""
   n = 0
   for u in _walk(t):
-    if u.op in REDUCE or u.op == "picked" or (u.op == "matmul" and not acc_ok): continue
+    if u.op in REDUCE or u.op in ROWWISE or u.op == "picked" or (u.op == "matmul" and not acc_ok): continue
     if u.op == "matmul": n += 1; continue
     n += 1
   return n
@@ -550,7 +568,7 @@ def _fit_program(root, shape, allow_acc):
     for u in _walk(root):
       for s in u.srcs: readers[id(s)] = readers.get(id(s), 0) + 1
     for u in list(_walk(root)):  # reductions (a reduction's own operand too), picked matmuls, and every matmul but
-      if u.op in REDUCE or u.op == "picked": u.realize()  # the root's chain's first are realized apart
+      if u.op in REDUCE or u.op in ROWWISE or u.op == "picked": u.realize()  # the root's chain's first are realized apart
     accs = [u for u in _walk(root) if u.op == "matmul"]
     for i, u in enumerate(accs):
       if not allow_acc or i > 0 or readers.get(id(u), 0) > 1 or u.shape != tuple(shape): u.realize()

@@ -287,6 +287,13 @@ int fh_matmul(const void* a, int a_dtype, int64_t a_batch_stride, int64_t lda, c
 int fh_reduce(const fh_program* program, int kind, int axis, int64_t batch, int64_t rows, int64_t cols, void* out,
               int out_dtype, void* stream);
 
+/* Along each row of the program's values over (batch, rows, cols): softmax, exp(x - max) / sum exp(x - max), or with
+ * log_form (x - max) - log sum exp(x - max), into out [batch][rows][cols] (FH_F32 or FH_BF16, nearest even):
+ * Tensor.softmax / log_softmax along the last axis (ferrite/tensor.py:433-437) in one launch, the elementwise tree under
+ * it evaluated in the same kernel. */
+int fh_softmax_rows(const fh_program* program, int log_form, int64_t batch, int64_t rows, int64_t cols, void* out,
+                    int out_dtype, void* stream);
+
 /* For each row of x[rows][n] (fp32), its largest value's column (the first of equals), into ids[rows]: greedy
  * decoding's pick (models/llama.py:792, numpy's argmax). */
 int fh_argmax_rows(const float* x, int64_t rows, int64_t n, int32_t* ids, void* stream);

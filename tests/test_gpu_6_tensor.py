@@ -111,6 +111,21 @@ def test_softmax_family(rt):
   e = np.exp(a - a.max(-1, keepdims=True))
   close(t.softmax().numpy(), e / e.sum(-1, keepdims=True), 1e-5, "softmax")
   close(t.log_softmax().numpy(), np.log(e / e.sum(-1, keepdims=True)), 1e-5, "log_softmax")
+  # along the last axis one launch, the elementwise tree under it in the same kernel; the composed form (another axis)
+  # agrees; bf16 rows round their sum as the composed form's bf16 sum does
+  before = rt.launches
+  got = (t * 0.5 + 1.0).softmax().numpy()
+  assert rt.launches - before == 1, rt.launches - before
+  e2 = np.exp(a * 0.5 - (a * 0.5).max(-1, keepdims=True))
+  close(got, e2 / e2.sum(-1, keepdims=True), 1e-5, "fused softmax")
+  tt = Tn().of(rt, np.swapaxes(a, 1, 2)[0].tolist(), "fp32")
+  close(tt.softmax(axis=1).numpy(), np.swapaxes(e / e.sum(-1, keepdims=True), 1, 2), 1e-5, "softmax down the rows")
+  b = Tn().of(rt, a[0].tolist(), "bf16")
+  ab = O.bf16(a).astype(np.float64)
+  eb = np.exp(ab - ab.max(-1, keepdims=True))
+  want = eb / O.bf16(eb.sum(-1, keepdims=True)).astype(np.float64)
+  close(b.softmax().numpy(), O.bf16(want), 2 ** -7, "bf16 softmax")
+  close(b.log_softmax().numpy(), O.bf16(np.log(want)), 2 ** -7, "bf16 log_softmax")
   c = a - a.mean(-1, keepdims=True)
   close(t.layernorm().numpy(), c / np.sqrt((c * c).mean(-1, keepdims=True) + 1e-5), 1e-4, "layernorm")
 
@@ -118,7 +133,7 @@ def test_softmax_family(rt):
 @pytest.mark.parametrize("rows", [1, 16, 200])
 def test_matmul_and_its_chain(rt, rows):
   # bf16 rows @ a bfp8 weight, then bias, relu and a row softmax: the matmul and its elementwise chain one kernel,
-  # the softmax's two reductions and its division three more
+  # the softmax one more
   rng = np.random.default_rng(66)
   K, N = 576, 1536
   x = O.bf16(rng.normal(0, 1, (rows, K)))
@@ -138,7 +153,9 @@ def test_matmul_and_its_chain(rt, rows):
   assert (err <= bound).all(), ("matmul", rows, float((err / bound).max()))
   # the softmax of an fp32 matmul's chain: its two reductions realize the matmul apart (fp32, so nothing rounds to
   # bf16 between them); within exp's growth of the sums' fp32 error
+  before = rt.launches
   s = (X.matmul(W, "fp32") + Bias).relu().softmax().numpy()[0]
+  assert rt.launches - before == 2, rt.launches - before  # the matmul with its chain, then the softmax
   e = np.exp(want - want.max(-1, keepdims=True))
   close(s, e / e.sum(-1, keepdims=True), 1e-4, ("softmax", rows))
 
