@@ -96,7 +96,9 @@ using namespace fh;
 extern "C" int fh_map(const fh_program* program, void* out, int out_dtype, int64_t batch, int64_t rows, int64_t cols,
                       int64_t ldb, int64_t ldo, void* stream) {
   if (int rc = check_program("fh_map", program, false)) return rc;
-  if (!out || batch < 1 || rows < 1 || cols < 1 || ldo < cols || ldb < rows * ldo) return fail(FH_EINVAL, "fh_map: bad shape or strides");
+  // (each output element its own place: matrices one after another, or interleaved row by row: a merge's view)
+  const bool apart = batch == 1 || ldb >= rows * ldo || (ldb >= cols && ldo >= batch * ldb);
+  if (!out || batch < 1 || rows < 1 || cols < 1 || ldo < cols || ldb < 0 || !apart) return fail(FH_EINVAL, "fh_map: bad shape or strides");
   if (out_dtype != FH_F32 && out_dtype != FH_BF16 && out_dtype != FH_I32) return fail(FH_EINVAL, "fh_map: out is FH_F32, FH_BF16 or FH_I32");
   hipLaunchKernelGGL(map_kernel, dim3(grid_for(batch * rows * cols)), dim3(256), 0, as_stream(stream), *program, out,
                      out_dtype, batch, rows, cols, ldb, ldo);

@@ -69,6 +69,8 @@ SIGNATURES = {
   "fh_heads_workspace_bytes": ([I, L, I], S),
   "fh_logit_heads": ([P, L, I, L, I, P, P, P, P, P, S, P], I),
   "fh_gather_cols": ([P, L, L, P, L, L, L, P, L, P], I),
+  "fh_gather_rows": ([P, L, L, L, P, L, L, L, P, L, L, P], I),
+  "fh_put_rows": ([P, L, L, L, P, L, L, L, P, L, L, P], I),
 }
 
 _lib = None

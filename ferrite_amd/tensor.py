@@ -198,6 +198,132 @@ class Tensor:
     st = x.data.stride()
     return x._view(tuple(map(len, rng)), sum(g.start * s for g, s in zip(rng, st)), tuple(g.step * s for g, s in zip(rng, st)))
 
+  def permute(self, *order):
+    """The axes in a new order, read in place (ferrite/tensor.py:186-190: swapping rows and columns is the transpose)."""
+    assert sorted(order) == [0, 1, 2]
+    if tuple(order) == (0, 1, 2): return self
+    x = self.realize()
+    st = x.data.stride()
+    return x._view(tuple(self.shape[k] for k in order), 0, tuple(st[k] for k in order))
+
+  def split(self, n, axis=2):
+    """The matrix cut into n equal parts along axis (2: columns, 1: rows) as a batch of n, read in place
+    (ferrite/tensor.py:218-229: attention's heads; by rows, each matrix of a batch too, its parts one after another)."""
+    assert axis in (1, 2)
+    x = self.realize()
+    if axis == 2:
+      assert self.batch == 1 and self.cols % n == 0, "equal parts of one matrix"
+      st = x.data.stride()
+      return x._view((n, self.rows, self.cols // n), 0, (self.cols // n * st[2], st[1], st[2]))
+    assert self.rows % n == 0, "equal parts"
+    if not x.data.is_contiguous(): x = (x + 0).realize()
+    return x._view((self.batch * n, self.rows // n, self.cols), 0, (self.rows // n * self.cols, self.cols, 1))
+
+  def merge(self):
+    """The batch side by side as one matrix, split's inverse (ferrite/tensor.py:231-236): x.split(n).merge() is x."""
+    out = Tensor._empty(self.rt, 1, self.rows, self.batch * self.cols, self.dtype)
+    view = out._view((self.batch, self.rows, self.cols), 0, (self.cols, self.batch * self.cols, 1))
+    self.realize(into=view)
+    return out
+
+  def pad(self, widths):
+    """Zeros around: (before, after) for each of the last len(widths) axes, as numpy's (ferrite/tensor.py:196-199)."""
+    widths = ((0, 0),) * (3 - len(widths)) + tuple(widths)
+    shape = tuple(n + w[0] + w[1] for n, w in zip(self.shape, widths))
+    out = Tensor._empty(self.rt, *shape, self.dtype, zero=True)
+    key = tuple(slice(w[0], w[0] + n) for w, n in zip(widths, self.shape))
+    self.realize(into=out[key])
+    return out
+
+  def cat(self, *xs, axis=0):
+    """Along axis, the other sizes the same (ferrite/tensor.py:201-208): each copied into its place in one tensor."""
+    ts, axis = (self, *xs), axis % 3
+    assert all(t.dtype == self.dtype and all(a == b for k, (a, b) in enumerate(zip(t.shape, self.shape)) if k != axis) for t in ts)
+    shape = list(self.shape)
+    shape[axis] = sum(t.shape[axis] for t in ts)
+    out, at = Tensor._empty(self.rt, *shape, self.dtype), 0
+    for t in ts:
+      key = [slice(None)] * 3
+      key[axis] = slice(at, at + t.shape[axis])
+      t.realize(into=out[tuple(key)])
+      at += t.shape[axis]
+    return out
+
+  def repeat_interleave(self, n):
+    """Each matrix n times over, one after another along the batch (numpy's repeat; ferrite/tensor.py:210-216: grouped-
+    query attention's keys and values, each head once for every query head it serves), as a copy."""
+    out = Tensor._empty(self.rt, self.batch * n, self.rows, self.cols, self.dtype)
+    for i in range(n): self.realize(into=out[i::n, :, :])
+    return out
+
+  def assign(self, x):
+    """x's value in this tensor (a stored tensor or a view of one), in place (ferrite/tensor.py:273-283)."""
+    assert self.data is not None and not isinstance(self.data, list) and self.dtype not in BFP, "a stored tensor or view"
+    assert (x.shape, x.dtype) == (self.shape, self.dtype), f"{x.shape} {x.dtype} into {self.shape} {self.dtype}"
+    x.realize(into=self)
+    return self
+
+  def gather(self, ids):
+    """Rows ids of this matrix, as a tensor (ferrite/tensor.py:116-126: an embedding lookup): ids an int32 tensor of
+    one row (read on the GPU, so it can be computed there) or a list. An index outside the rows reads the nearest. A
+    block float's rows are gathered packed (its runs' magnitudes and exponents)."""
+    if not isinstance(ids, Tensor):
+      assert all(0 <= i < self.rows for i in ids)
+      ids = Tensor.of(self.rt, [list(ids)], "int32")
+    assert self.batch == 1 and ids.dtype == "int32" and ids.shape[:2] == (1, 1), "rows of a matrix, by a row of int32"
+    idx, n = _ids(ids), ids.cols
+    x = self.realize()
+    if x.dtype in BFP:
+      (w,) = _matrices(x)
+      out = Tensor(self.rt, n, self.cols, dtype=self.dtype)
+      with self.rt.on(): g = ops.bfp_empty(n, w.N, w.fmt, device=self.rt.device)
+      rb, runs = (16 if w.fmt == "bfp8" else 8), w.N // 16
+      self.rt.run(lambda: (lib.call("fh_gather_rows", ops._ptr(w.mant), w.K, rb, w.K * rb, ops._ptr(idx), n, rb, runs, ops._ptr(g.mant), rb, n * rb, ops._stream()),
+                           lib.call("fh_gather_rows", ops._ptr(w.exps), w.K, 1, w.K, ops._ptr(idx), n, 1, runs, ops._ptr(g.exps), 1, n, ops._stream())), "gather")
+      out.data = g
+      return out
+    if x.data.stride(2) != 1: x = (x + 0).realize()
+    es, st = ITEMSIZE[self.dtype], x.data.stride()
+    out = Tensor._empty(self.rt, 1, n, self.cols, self.dtype)
+    self.rt.run(lambda: lib.call("fh_gather_rows", ops._ptr(x.data), self.rows, st[1] * es, 0, ops._ptr(idx), n, self.cols * es, 1,
+                                 ops._ptr(out.data), self.cols * es, 0, ops._stream()), "gather")
+    return out
+
+  def put(self, ids, x):
+    """x's rows into rows ids of each matrix of this tensor, in place, gather's inverse (ferrite/tensor.py:128-140: a KV
+    cache takes a token's keys at its place): ids an int32 tensor of one row, read on the GPU. Into a block float, x is
+    bf16, each of its runs of 16 rounded as cast rounds them (fh_bfp_pack), then its packed rows put in place. An index
+    outside the rows writes nothing."""
+    assert ids.dtype == "int32" and ids.shape[:2] == (1, 1) and ids.cols == x.rows, "rows of x, by a row of int32 places"
+    assert (x.batch, x.cols) == (self.batch, self.cols) and x.dtype == ("bf16" if self.dtype in BFP else self.dtype), \
+      f"{x.shape} {x.dtype} into {self.shape} {self.dtype}"
+    assert self.data is not None, "into a stored tensor"
+    idx, n = _ids(ids), x.rows
+    xr = x.realize()
+    if not xr.data.is_contiguous(): xr = (xr + 0).realize()
+    if self.dtype in BFP:
+      for b, w in enumerate(_matrices(self)):
+        rb, runs = (16 if w.fmt == "bfp8" else 8), w.N // 16
+        p = self.rt.run(lambda b=b, w=w: ops.pack(xr.data[b], w.fmt), "pack")
+        self.rt.run(lambda w=w, p=p: (lib.call("fh_put_rows", ops._ptr(w.mant), w.K, rb, w.K * rb, ops._ptr(idx), n, rb, runs, ops._ptr(p.mant), rb, n * rb, ops._stream()),
+                                      lib.call("fh_put_rows", ops._ptr(w.exps), w.K, 1, w.K, ops._ptr(idx), n, 1, runs, ops._ptr(p.exps), 1, n, ops._stream())), "put")
+      return self
+    assert self.data.stride(2) == 1, "into rows of contiguous elements"
+    es, st = ITEMSIZE[self.dtype], self.data.stride()
+    self.rt.run(lambda: lib.call("fh_put_rows", ops._ptr(self.data), self.rows, st[1] * es, st[0] * es, ops._ptr(idx), n, self.cols * es,
+                                 self.batch, ops._ptr(xr.data), self.cols * es, n * self.cols * es, ops._stream()), "put")
+    return self
+
+  @classmethod
+  def _empty(cls, rt, batch, rows, cols, dtype, zero=False):
+    """A stored tensor of its own memory (zeros by our fill kernel if asked)."""
+    with rt.on(): t = torch.empty(batch, rows, cols, dtype=TORCH[dtype], device=rt.device)
+    out = cls._stored(rt, t, dtype)
+    if zero:
+      p = _cprogram([("copy", lib.OPND_IMM, lib.OPND_IMM, 0.0)], [])
+      rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(t), DT[dtype], batch, rows, cols, rows * cols, cols, ops._stream()), "map")
+    return out
+
   def expand(self, *shape):  # dimensions of 1 repeated (a stride of 0), missing ones in front being 1
     shape = (1,) * (3 - len(shape)) + shape
     assert all(n in (m, 1) for n, m in zip(self.shape, shape)), f"cannot expand {self.shape} to {shape}"
@@ -406,7 +532,7 @@ class Tensor:
     dtype, rows contiguous: jit's copies of its inputs); returns it, realized."""
     if into is not None:
       assert into.data is not None and into.shape == self.shape and into.dtype == self.dtype and into.dtype not in BFP
-      assert into.data.is_contiguous(), "realize(into=): a tensor of its own memory"
+      assert into.data.stride(2) == 1 or into.cols == 1, "realize(into=): rows contiguous"
       if self is into: return into
       prog, inputs = _fit_program(self, self.shape, allow_acc=False)  # (a stored tensor: one copy op)
       p = _cprogram(prog, inputs)
@@ -468,6 +594,12 @@ class Tensor:
 
   def _done(self, data):
     self.data, self.op, self.srcs, self.args = data, None, (), ()
+
+
+def _ids(ids):
+  """An int32 row tensor's values on the GPU, contiguous."""
+  d = ids.realize().data
+  return d if d.is_contiguous() else (ids + 0).realize().data
 
 
 def _matrices(t):

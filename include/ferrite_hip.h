@@ -266,7 +266,7 @@ int fh_moe_experts(const float* x, int64_t ldx, int rows, int64_t dim, const flo
 /* ---- lazy tensors' kernels (ferrite/tensor.py: elementwise trees, reductions) ---------------------------------- */
 
 /* out[b][r][c] = program at (b, r, c), out's dtype FH_F32, FH_BF16 (nearest even) or FH_I32; out rows ldo apart,
- * batches ldb apart. Replaces fused_kernel for an elementwise tree (ferrite/compiler.py:699). */
+ * batches ldb apart (matrices one after another, ldb >= rows ldo, or interleaved row by row, ldo >= batch ldb). Replaces fused_kernel for an elementwise tree (ferrite/compiler.py:699). */
 int fh_map(const fh_program* program, void* out, int out_dtype, int64_t batch, int64_t rows, int64_t cols, int64_t ldb,
            int64_t ldo, void* stream);
 
@@ -319,6 +319,16 @@ int fh_logit_heads(const float* logits, int64_t ldl, int rows, int64_t vocab, in
  * (ferrite/tensor.py:373-388, topk_kernel's labels, compiler.py:1716-1838). */
 int fh_gather_cols(const void* src, int64_t lds, int64_t cols, const int32_t* idx, int64_t ldi, int64_t rows, int64_t k,
                    void* out, int64_t ldo, void* stream);
+
+/* ---- rows by index (Tensor.gather / Tensor.put, ferrite/tensor.py:116-140) ----------------------------------
+ * Rows of bytes in planes (a batch's matrices, or a block float's runs of 16 columns: its magnitudes' and exponents'
+ * planes). Sizes and strides in bytes. gather: out[p][j] = src[p][ids[j]], an index outside [0, src_rows) read at the
+ * nearest row; put: dst[p][ids[j]] = src[p][j], an index outside [0, dst_rows) writing nothing. A put with an index
+ * twice writes one of the two rows. */
+int fh_gather_rows(const void* src, int64_t src_rows, int64_t src_ld, int64_t src_plane, const int32_t* ids, int64_t n,
+                   int64_t row_bytes, int64_t planes, void* out, int64_t out_ld, int64_t out_plane, void* stream);
+int fh_put_rows(void* dst, int64_t dst_rows, int64_t dst_ld, int64_t dst_plane, const int32_t* ids, int64_t n,
+                int64_t row_bytes, int64_t planes, const void* src, int64_t src_ld, int64_t src_plane, void* stream);
 
 /* ---- measurement ------------------------------------------------------------------------------------------
  * The read floor a matmul's weight stream is measured against (bench.py's read_floor): `bytes` (a multiple of 16) of
