@@ -314,6 +314,36 @@ class Tensor:
                                  self.batch, ops._ptr(xr.data), self.cols * es, n * self.cols * es, ops._stream()), "put")
     return self
 
+  def attend(self, k, v, places, window=0, fidelity=None, parts=None):
+    """softmax(self @ k^T + mask) @ v (ferrite/tensor.py:487-516): self a batch of query rows (bf16 or fp32; scaled by
+    the caller), k and v the keys and values for each matrix (bf16, fp32 or a block float: a KV cache's, whose values
+    are bf16 values, read as those), places an int32 column (batch 1 or self's): row t sees keys up to places[t], and
+    with a window, none window or more before it. Scores and sums in fp32; the result bf16 (fh_attend). fidelity and
+    parts (ferrite's product phases and its workers' share of the keys) are taken and ignored: one kernel reads every
+    key a row sees."""
+    assert self.dtype in ("bf16", "fp32") and k.dtype == v.dtype and k.dtype != "int32" and self.batch == k.batch == v.batch
+    assert self.cols == k.cols == v.cols and k.rows == v.rows and self.cols <= 256, f"{self.shape} by {k.shape}, {v.shape}"
+    assert places.rows == self.rows and places.cols == 1 and places.batch in (1, self.batch) and places.dtype == "int32", \
+      f"{self.shape} by {k.shape}, {places.shape}"
+    def plain(t):  # a block float as its bf16 values (exact); rows of contiguous elements
+      x = t.realize()
+      if x.dtype in BFP:
+        out = Tensor._empty(self.rt, x.batch, x.rows, x.cols, "bf16")
+        for b, w in enumerate(_matrices(x)): self.rt.run(lambda b=b, w=w: ops.dequant(w, out.data[b]), "dequant")
+        return out
+      return x if x.data.stride(2) == 1 else (x + 0).realize()
+    q, k, v = plain(self), plain(k), plain(v)
+    if k.dtype != v.dtype: k, v = k.float().realize(), v.float().realize()
+    pl = places.realize()
+    if not pl.data.is_contiguous(): pl = (pl + 0).realize()
+    out = Tensor._empty(self.rt, self.batch, self.rows, self.cols, "bf16")
+    qs, ks, vs, os_ = (t.data.stride() for t in (q, k, v, out))
+    self.rt.run(lambda: lib.call("fh_attend", ops._ptr(q.data), DT[q.dtype], qs[0], qs[1], ops._ptr(k.data), ops._ptr(v.data), DT[k.dtype],
+                                 ks[0], ks[1], vs[0], vs[1], k.rows, self.batch, self.rows, self.cols, ops._ptr(pl.data),
+                                 self.rows if pl.batch > 1 else 0, int(window), ops._ptr(out.data), lib.BF16, os_[0], os_[1],
+                                 ops._stream()), "attention")
+    return out
+
   @classmethod
   def _empty(cls, rt, batch, rows, cols, dtype, zero=False):
     """A stored tensor of its own memory (zeros by our fill kernel if asked)."""

@@ -320,6 +320,17 @@ int fh_logit_heads(const float* logits, int64_t ldl, int rows, int64_t vocab, in
 int fh_gather_cols(const void* src, int64_t lds, int64_t cols, const int32_t* idx, int64_t ldi, int64_t rows, int64_t k,
                    void* out, int64_t ldo, void* stream);
 
+/* Attention of a batch of query rows (Tensor.attend, ferrite/tensor.py:487-516): out[b][t] = softmax(q[b][t] k[b]^T +
+ * mask) v[b] with q [batch][T][head_dim], k and v [batch][S][head_dim] (rows ld* apart, batches *_batch_stride apart,
+ * q, k and v FH_BF16 or FH_F32, k and v alike), the scores in fp32; row t sees keys places[b][t] - window + 1 ..
+ * places[b][t] (window 0: from key 0), clipped to the keys there are; a row seeing none is zeros. places int32, a
+ * batch's places_batch_stride apart (0: one column for every matrix). head_dim up to 256. out FH_BF16 (nearest even) or
+ * FH_F32. The general form; a decode step's attention over its KV cache is fh_attention_decode. */
+int fh_attend(const void* q, int q_dtype, int64_t q_batch_stride, int64_t ldq, const void* k, const void* v, int kv_dtype,
+              int64_t k_batch_stride, int64_t ldk, int64_t v_batch_stride, int64_t ldv, int64_t S, int batch, int64_t T,
+              int head_dim, const int32_t* places, int64_t places_batch_stride, int64_t window, void* out, int out_dtype,
+              int64_t out_batch_stride, int64_t ldo, void* stream);
+
 /* ---- rows by index (Tensor.gather / Tensor.put, ferrite/tensor.py:116-140) ----------------------------------
  * Rows of bytes in planes (a batch's matrices, or a block float's runs of 16 columns: its magnitudes' and exponents'
  * planes). Sizes and strides in bytes. gather: out[p][j] = src[p][ids[j]], an index outside [0, src_rows) read at the

@@ -104,3 +104,49 @@ def test_put_into_block_float(rt, fmt):
   assert np.array_equal(got, want.astype(np.float32))
   # its packed rows gathered back: the same values
   assert np.array_equal(cache.gather([60, 0]).numpy()[0], want[[60, 0]].astype(np.float32))
+
+
+def _attend_np(q, k, v, places, window):
+  B, T, hd = q.shape
+  out = np.zeros((B, T, hd))
+  for b in range(B):
+    for t in range(T):
+      p = places[b if places.shape[0] > 1 else 0, t, 0]
+      hi, lo = min(p, k.shape[1] - 1), (max(p - window + 1, 0) if window else 0)
+      if hi < lo: continue
+      s = q[b, t].astype(np.float64) @ k[b, lo:hi + 1].T.astype(np.float64)
+      e = np.exp(s - s.max())
+      out[b, t] = e @ v[b, lo:hi + 1] / e.sum()
+  return out
+
+
+@pytest.mark.parametrize("hd", [64, 96, 128])
+def test_attend(rt, hd):
+  # Tensor.attend as models/llama.py:134-139 calls it: q scaled by 1/sqrt(hd), a batch of heads, each row's place, with
+  # and without a window; keys and values bf16, fp32, or a block float (a KV cache's bfp8 values, read as those); grouped
+  # query heads by repeat_interleave
+  rng = np.random.default_rng(146 + hd)
+  B, T, S = 4, 6, 70
+  q = O.bf16(rng.normal(0, 1, (B, T, hd)))
+  k, v = O.bf16(rng.normal(0, 1, (B, S, hd))), O.bf16(rng.normal(0, 1, (B, S, hd)))
+  places = rng.integers(0, S + 5, (1, T, 1)).astype(np.int32)  # (some past the keys: clipped)
+  scale = 1 / np.sqrt(hd)
+  Q, K, V, Pl = Tn().of(rt, q.tolist()), Tn().of(rt, k.tolist()), Tn().of(rt, v.tolist()), Tn().of(rt, places[0].tolist(), "int32")
+  for window in (0, 9):
+    got = (Q * scale).attend(K, V, Pl, window).numpy()
+    want = _attend_np(O.bf16(q * scale), k, v, places, window)
+    assert np.abs(got - want).max() <= 2 ** -7 * np.abs(want).max(), (hd, window)
+  # fp32 keys and values; places a column for each matrix
+  pb = rng.integers(0, S, (B, T, 1)).astype(np.int32)
+  got = (Q * scale).attend(K.float(), V.float(), Tn().of(rt, pb.tolist(), "int32")).numpy()
+  assert np.abs(got - _attend_np(O.bf16(q * scale), k, v, pb, 0)).max() <= 2 ** -7 * 4
+  # a bfp8 cache: the same as attending over its values in bf16
+  Kc, Vc = Tn().of(rt, k.tolist()).cast("bfp8"), Tn().of(rt, v.tolist()).cast("bfp8")
+  got = (Q * scale).attend(Kc, Vc, Pl).numpy()
+  want = _attend_np(O.bf16(q * scale), np.stack([O.bfp(m) for m in k]), np.stack([O.bfp(m) for m in v]), places, 0)
+  assert np.abs(got - want).max() <= 2 ** -7 * np.abs(want).max()
+  # grouped-query: 2 key heads serving 4 query heads
+  K2, V2 = Tn().of(rt, k[:2].tolist()), Tn().of(rt, v[:2].tolist())
+  got = (Q * scale).attend(K2.repeat_interleave(2), V2.repeat_interleave(2), Pl).numpy()
+  want = _attend_np(O.bf16(q * scale), np.repeat(k[:2], 2, 0), np.repeat(v[:2], 2, 0), places, 0)
+  assert np.abs(got - want).max() <= 2 ** -7 * np.abs(want).max()
