@@ -70,6 +70,8 @@ SIGNATURES = {
   "fh_logit_heads": ([P, L, I, L, I, P, P, P, P, P, S, P], I),
   "fh_gather_cols": ([P, L, L, P, L, L, L, P, L, P], I),
   "fh_gather_rows": ([P, L, L, L, P, L, L, L, P, L, L, P], I),
+  "fh_moe_touched": ([P, L, P, L, I, I, I, P, P, P], I),
+  "fh_moe_group": ([P, L, I, I, I, P, P, P, P, P], I),
   "fh_attend": ([P, I, L, L, P, P, I, L, L, L, L, L, I, L, I, P, L, L, P, I, L, L, P], I),
   "fh_put_rows": ([P, L, L, L, P, L, L, L, P, L, L, P], I),
 }

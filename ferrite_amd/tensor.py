@@ -344,6 +344,39 @@ class Tensor:
                                  ops._stream()), "attention")
     return out
 
+  def touched(self, n, weights):
+    """A mixture of experts' choices (int32, rows x k, values below n) as the experts some row picks by a weight not 0,
+    each once, and each such entry's weight from each row (ferrite/tensor.py:403-416): experts, a column of
+    min(rows k, n), those picked in increasing order then n (none); weights (that many, rows, 1) bf16, 0 for a row that
+    did not pick the entry's expert. A decode step's few tokens then go through each picked expert once (matmul by
+    index=experts). By fh_moe_touched."""
+    assert self.dtype == "int32" and weights.dtype == "bf16" and self.shape == weights.shape and self.batch == 1
+    rows, k = self.rows, self.cols
+    slots = min(rows * k, n)
+    x, w = (t.realize() if t.realize().data.stride(2) == 1 else (t + 0).realize() for t in (self, weights))
+    experts = Tensor._empty(self.rt, 1, slots, 1, "int32")
+    out = Tensor._empty(self.rt, slots, rows, 1, "bf16")
+    self.rt.run(lambda: lib.call("fh_moe_touched", ops._ptr(x.data), x.data.stride(1), ops._ptr(w.data), w.data.stride(1), rows, k, n,
+                                 ops._ptr(experts.data), ops._ptr(out.data), ops._stream()), "touched")
+    return experts, out
+
+  def group(self, n):
+    """A mixture of experts' tokens grouped by expert (ferrite/tensor.py:389-402), from int32 choices (rows x k, values
+    below n): order, a row of 32 t slots in which each value's choices have a run of whole tiles of 32 (each slot the
+    row it holds, 0 for none); tiles, a column of t, each tile's value (n past those used); places, a row of k runs of
+    the rows rounded up to 32, run j holding the slot of each row's choice j. Each expert's tokens are then a batch entry
+    of whole tiles for a matmul that picks its weights (index=tiles). By fh_moe_group."""
+    assert self.dtype == "int32" and self.batch == 1, "a matrix of int32 choices"
+    rows, k = self.rows, self.cols
+    t, rp = -(-rows * k // 32) + min(n, rows * k), -(-rows // 32) * 32
+    x = self.realize()
+    if x.data.stride(2) != 1: x = (x + 0).realize()
+    order, tiles, places = (Tensor._empty(self.rt, 1, r, c, "int32") for r, c in ((1, 32 * t), (t, 1), (1, k * rp)))
+    with self.rt.on(): fill = torch.empty(n, dtype=torch.int32, device=self.rt.device)
+    self.rt.run(lambda: lib.call("fh_moe_group", ops._ptr(x.data), x.data.stride(1), rows, k, n, ops._ptr(order.data), ops._ptr(tiles.data),
+                                 ops._ptr(places.data), ops._ptr(fill), ops._stream()), "group")
+    return order, tiles, places
+
   @classmethod
   def _empty(cls, rt, batch, rows, cols, dtype, zero=False):
     """A stored tensor of its own memory (zeros by our fill kernel if asked)."""

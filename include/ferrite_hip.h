@@ -331,6 +331,19 @@ int fh_attend(const void* q, int q_dtype, int64_t q_batch_stride, int64_t ldq, c
               int head_dim, const int32_t* places, int64_t places_batch_stride, int64_t window, void* out, int out_dtype,
               int64_t out_batch_stride, int64_t ldo, void* stream);
 
+/* A mixture of experts' choices ids [rows][k] (int32, values below n, rows ldi apart) as the lists an indexed matmul
+ * takes (Tensor.touched / Tensor.group, ferrite/tensor.py:389-416; compiler.py:1842-1945). touched: experts [slots]
+ * (slots = min(rows k, n)) the experts some row picks by a weight whose bits are not 0 (weights_in [rows][k] bf16, ldw
+ * apart), increasing, then n; weights [slots][rows] bf16, the weight row r gave entry s's expert (0 if it did not pick
+ * it). group: t = ceil(rows k / 32) + min(n, rows k) tiles of 32 slots, each value's choices a run of whole tiles after
+ * the runs of the values before it, each choice (row by row, a row's in turn) the next slot of its value's run;
+ * order [32 t] the row each slot holds (0 for none), tiles [t] each tile's value (n past those used), places
+ * [k][rp] (rp = rows rounded up to 32) the slot of row r's choice j (0 past the rows). workspace: n int32. */
+int fh_moe_touched(const int32_t* ids, int64_t ldi, const uint16_t* weights_in, int64_t ldw, int rows, int k, int n,
+                   int32_t* experts, uint16_t* weights, void* stream);
+int fh_moe_group(const int32_t* ids, int64_t ldi, int rows, int k, int n, int32_t* order, int32_t* tiles, int32_t* places,
+                 int32_t* workspace, void* stream);
+
 /* ---- rows by index (Tensor.gather / Tensor.put, ferrite/tensor.py:116-140) ----------------------------------
  * Rows of bytes in planes (a batch's matrices, or a block float's runs of 16 columns: its magnitudes' and exponents'
  * planes). Sizes and strides in bytes. gather: out[p][j] = src[p][ids[j]], an index outside [0, src_rows) read at the

@@ -150,3 +150,45 @@ def test_attend(rt, hd):
   got = (Q * scale).attend(K2.repeat_interleave(2), V2.repeat_interleave(2), Pl).numpy()
   want = _attend_np(O.bf16(q * scale), np.repeat(k[:2], 2, 0), np.repeat(v[:2], 2, 0), places, 0)
   assert np.abs(got - want).max() <= 2 ** -7 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("dense", [True, False])
+def test_experts_by_touched_and_group(rt, dense):
+  # models/llama.py:302-329's chip_experts on this Tensor, both ways: each picked expert once with every token its rows
+  # (touched; a decode step's), or each expert's tokens grouped into whole tiles of 32 (group; a prompt's), gathered
+  # back and weighted; against numpy_experts (llama.py:294-300) over the same bf16 rows and block-float experts
+  rng = np.random.default_rng(147)
+  rows, dim, m, e, k = 40, 64, 96, 8, 2
+  h = O.bf16(rng.normal(0, 1, (rows, dim)))
+  ids = np.stack([rng.choice(e - 1, k, replace=False) for _ in range(rows)]).astype(np.int32)  # (a row's experts distinct,
+                                                                                              # as topk's; expert 7 picked
+                                                                                              # by none: an entry is none)
+  w = O.bf16(rng.uniform(0.1, 1, (rows, k)))
+  gu = rng.normal(0, 0.05, (e, dim, 2 * m)).astype(np.float32)
+  dn = rng.normal(0, 0.05, (e, m, dim)).astype(np.float32)
+  H, Ids, W = Tn().of(rt, h.tolist()), Tn().of(rt, ids.tolist(), "int32"), Tn().of(rt, w.tolist())
+  GU, DN = Tn().of(rt, gu.tolist(), "fp32").cast("bfp8"), Tn().of(rt, dn.tolist(), "fp32").cast("bfp8")
+  glu = lambda g: g[:, :, :m].silu() * g[:, :, m:]
+  if dense:
+    picks, weights = Ids.touched(e, W)
+    assert picks.numpy().ravel().tolist() == sorted(set(ids.ravel().tolist())) + [e] * (min(rows * k, e) - len(set(ids.ravel().tolist())))
+    got = (glu(H.matmul(GU, index=picks)) * weights).matmul(DN, index=picks).sum(0).numpy()[0]
+  else:
+    order, picks, places = Ids.group(e)
+    x = H.gather(order).split(picks.rows, 1)
+    y = glu(x.matmul(GU, index=picks)).matmul(DN, index=picks).reshape(order.cols, dim)
+    run = places.cols // k
+    terms = [y.gather(places[:, :, j * run:j * run + rows]) * W[:, :, j:j + 1] for j in range(k)]
+    got = (terms[0] + terms[1]).numpy()[0]
+    o = order.numpy().ravel()
+    for t in range(rows):  # every choice has a slot holding its row, in its value's run
+      for j in range(k):
+        s = places.numpy().ravel()[j * run + t]
+        assert o[s] == t and picks.numpy().ravel()[s // 32] == ids[t, j]
+  gv, dv = np.stack([O.bfp(a) for a in gu]), np.stack([O.bfp(a) for a in dn])
+  silu = lambda a: a / (1 + np.exp(-a))
+  def expert(x, i):
+    g = O.bf16(x.astype(np.float64) @ gv[i]).astype(np.float64)
+    return O.bf16(O.bf16(silu(g[:m])) * g[m:]).astype(np.float64) @ dv[i]
+  want = np.stack([sum(w[t, j] * expert(h[t], ids[t, j]) for j in range(k)) for t in range(rows)])
+  assert np.abs(got - want).max() <= 2 ** -6 * np.abs(want).max(), np.abs(got - want).max() / np.abs(want).max()
