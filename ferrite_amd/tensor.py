@@ -258,6 +258,7 @@ class Tensor:
 
   def assign(self, x):
     """x's value in this tensor (a stored tensor or a view of one), in place (ferrite/tensor.py:273-283)."""
+    if self.op is None: self.realize()  # (one made empty: its memory)
     assert self.data is not None and not isinstance(self.data, list) and self.dtype not in BFP, "a stored tensor or view"
     assert (x.shape, x.dtype) == (self.shape, self.dtype), f"{x.shape} {x.dtype} into {self.shape} {self.dtype}"
     x.realize(into=self)
@@ -297,6 +298,7 @@ class Tensor:
     assert ids.dtype == "int32" and ids.shape[:2] == (1, 1) and ids.cols == x.rows, "rows of x, by a row of int32 places"
     assert (x.batch, x.cols) == (self.batch, self.cols) and x.dtype == ("bf16" if self.dtype in BFP else self.dtype), \
       f"{x.shape} {x.dtype} into {self.shape} {self.dtype}"
+    self.realize()  # (one made empty: its memory)
     assert self.data is not None, "into a stored tensor"
     idx, n = _ids(ids), x.rows
     xr = x.realize()
@@ -603,6 +605,10 @@ class Tensor:
       self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[into.dtype], *into.shape, ld[0], ld[1], ops._stream()), "map")
       return into
     if self.data is not None: return self
+    if self.op is None:  # made empty (ferrite's Tensor(rt, rows, cols, batch, dtype), the model's `empty`): its memory now
+      assert self.dtype not in BFP, "a block float is made by cast"
+      with self.rt.on(): self.data = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
+      return self
     if self.op == "picked":
       self._done(_picked(self).data)
       return self
@@ -799,6 +805,7 @@ def _emit(t, shape, prog, inputs, regs):
     t._acc = True
     regs[id(t)] = lib.OPND_ACC
     return lib.OPND_ACC
+  if t.data is None and t.op is None: t.realize()  # (made empty: its memory)
   if t.data is not None or t.op is None: return _operand(t, shape, prog, inputs, regs)
   op = t.op
   if op == "cast" and t is not regs["root"] and t.dtype != "fp32":  # a rounding below the root: realized first, as

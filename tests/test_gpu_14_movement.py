@@ -54,6 +54,18 @@ def test_pad_cat_repeat(rt):
   assert i.pad(((1, 1),)).tolist() == [[0, 1, 2, 0], [0, 3, 4, 0]]
 
 
+def test_empty_then_filled(rt):
+  # the model's `empty` (models/llama.py:47): a tensor made with no value, its memory taken when first used
+  rng = np.random.default_rng(148)
+  e = Tn()(rt, 3, 4, batch=2, dtype="fp32")
+  y = rng.normal(0, 1, (2, 3, 4)).astype(np.float32)
+  e.assign(Tn().of(rt, y.tolist(), "fp32"))
+  assert np.array_equal(e.numpy(), y)
+  c = Tn()(rt, 5, 4, batch=2, dtype="fp32")
+  c.put(Tn().of(rt, [[4, 1, 0]], "int32"), Tn().of(rt, y.tolist(), "fp32"))
+  assert np.array_equal(c.numpy()[:, [4, 1, 0]], y)
+
+
 def test_assign_into_a_view(rt):
   rng = np.random.default_rng(143)
   a = rng.normal(0, 1, (2, 6, 7)).astype(np.float32)
