@@ -33,9 +33,12 @@ def test_decode_written_with_tensors(rt):
   def rms(x, g): return x * ((x * x).mean(2) + c.eps).rsqrt() * g
 
   def step(ids, places):
-    n = len(ids)
     at = Tensor.of(rt, [list(places)], "int32")           # the places as a row (put, gather) and a column (attend)
     col = Tensor.of(rt, [[p] for p in places], "int32")
+    return forward(Tensor.of(rt, [list(ids)], "int32"), at, col).numpy()[0]
+
+  def forward(ids, at, col):  # (tensors only: jit replays it with new ids and places)
+    n = ids.cols
     x = W["embed"].gather(ids)
     cs, sn = cos.gather(at).split(nh), sin.gather(at).split(nh)
     for l in range(c.layers):
@@ -50,13 +53,24 @@ def test_decode_written_with_tensors(rt):
       gu = rms(x, p("post_attention_layernorm")).matmul(p("gate_up_proj"), "fp32").realize()
       x = (x + (gu[:, :, :c.ffn].silu() * gu[:, :, c.ffn:]).matmul(p("down_proj"), "fp32")).realize()
     assert x.shape == (1, n, c.dim)
-    return rms(x, W["norm"]).matmul(W["embed.T"], "fp32").numpy()[0]
+    return rms(x, W["norm"]).matmul(W["embed.T"], "fp32")
+
+  def check(got, want, what):
+    rel = np.abs(got - want).max() / np.abs(want).max()
+    cosine = float(got @ want / (np.linalg.norm(got) * np.linalg.norm(want)))
+    assert rel <= 1e-2 and cosine >= 0.9999, (what, rel, cosine)
+    assert int(np.argmax(got)) == int(np.argmax(want)), what
 
   arrays, ocache = OL.arrays(w, c.precision), OL.kv_cache(c, size)
   for ids, places in (([5, 9, 200], [0, 1, 2]), ([77], [3])):
-    got = step(ids, places)[-1]
-    want = OL.forward(ids, places, arrays, c, ocache)[0]
-    rel = np.abs(got - want).max() / np.abs(want).max()
-    cosine = float(got @ want / (np.linalg.norm(got) * np.linalg.norm(want)))
-    assert rel <= 1e-2 and cosine >= 0.9999, (ids, rel, cosine)
-    assert int(np.argmax(got)) == int(np.argmax(want))
+    check(step(ids, places)[-1], OL.forward(ids, places, arrays, c, ocache)[0], ids)
+  # then greedy decoding with the step as ferrite's jit replays it (tensor.py:788-810): the first call runs, the second
+  # is captured as a HIP graph, later calls copy the token and its place in and replay; each pick fed back
+  from ferrite_amd import tensor
+  f = tensor.jit(forward)
+  token = 77
+  for place in range(4, 9):
+    want = OL.forward([token], [place], arrays, c, ocache)[0]
+    got = f(Tensor.of(rt, [[token]], "int32"), Tensor.of(rt, [[place]], "int32"), Tensor.of(rt, [[place]], "int32")).numpy()[0][-1]
+    check(got, want, ("jit", place))
+    token = int(np.argmax(want))
