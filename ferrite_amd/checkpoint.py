@@ -169,3 +169,69 @@ class Checkpoint:
     bf16 on the GPU."""
     name = f"layers.{layer}.router" if f"layers.{layer}.router" in self.tensors else f"layers.{layer}.gate"
     return self.gpu(name).to(torch.bfloat16).t().contiguous()
+
+
+_DT = {torch.uint8: "U8", torch.float32: "F32", torch.bfloat16: "BF16"}
+_NP = {"U8": np.uint8, "F32": np.float32, "BF16": np.uint16}
+
+
+def save_packed(dec, path):
+  """A Decoder's weights as it holds them, in one safetensors file (the packed-weights cache of models/llama.py's
+  upload path, llama.py:628-640, for this layout): each block-float matrix's magnitudes and exponents as U8 (its format,
+  K and N in the header's metadata), the norms as F32, the embedding as BF16. Packed(path) gives them back to a Decoder
+  without a checkpoint or a repacking; the KV cache and the step's buffers are not saved."""
+  tensors, meta = {}, {"format": "ferrite_amd packed", "mode": dec.mode}
+  for l, L in enumerate(dec.layers):
+    for op in ("qkv", "o", "gate_up", "down"):
+      name, bw = f"layers.{l}.{op}_proj", getattr(L, op)
+      tensors[name + ".mant"], tensors[name + ".exps"] = bw.mant, bw.exps
+      meta[name] = f"{bw.fmt} {bw.K} {bw.N}"
+    tensors[f"layers.{l}.input_layernorm"], tensors[f"layers.{l}.post_attention_layernorm"] = L.norm1, L.norm2
+  tensors["norm"], tensors["embed_tokens"] = dec.norm, dec.embed
+  tensors["embed.T.mant"], tensors["embed.T.exps"] = dec.head.mant, dec.head.exps
+  meta["embed.T"] = f"{dec.head.fmt} {dec.head.K} {dec.head.N}"
+  header, offset = {"__metadata__": meta}, 0
+  for name, t in tensors.items():
+    n = t.numel() * t.element_size()
+    header[name] = {"dtype": _DT[t.dtype], "shape": list(t.shape), "data_offsets": [offset, offset + n]}
+    offset += n
+  raw = json.dumps(header).encode()
+  raw += b" " * (-len(raw) % 8)
+  with open(path, "wb") as f:
+    f.write(struct.pack("<Q", len(raw)))
+    f.write(raw)
+    for t in tensors.values():  # (a tensor at a time through host memory)
+      c = t.detach().contiguous().cpu()
+      f.write((c.view(torch.int16) if c.dtype == torch.bfloat16 else c).numpy().tobytes())
+
+
+class Packed:
+  """A file save_packed wrote, for Decoder (as a Checkpoint): pack(name, fmt) gives the stored block float (which must
+  be in fmt), vector(name) a norm, table() the embedding, each copied to the GPU as stored."""
+
+  def __init__(self, path, device="cuda"):
+    self.device = torch.device(device)
+    with open(path, "rb") as f:
+      size = struct.unpack("<Q", f.read(8))[0]
+      header = json.loads(f.read(size))
+    self.meta = header.pop("__metadata__", {})
+    if self.meta.get("format") != "ferrite_amd packed": raise ValueError(f"{path}: not a file save_packed wrote")
+    self.header, self.data = header, np.memmap(path, np.uint8, "r", offset=8 + size)
+
+  def _gpu(self, name):
+    t = self.header[name]
+    raw = np.asarray(self.data[t["data_offsets"][0]:t["data_offsets"][1]]).view(_NP[t["dtype"]]).reshape(t["shape"])
+    x = torch.from_numpy(raw.copy())
+    return (x.view(torch.bfloat16) if t["dtype"] == "BF16" else x).to(self.device)
+
+  def pack(self, name, fmt):
+    if name not in self.meta: raise KeyError(f"packed file: no matrix {name}")
+    stored, K, N = self.meta[name].split()
+    if stored != fmt: raise ValueError(f"packed file: {name} is {stored}, the model's precision says {fmt}")
+    return ops.BfpWeight(self._gpu(name + ".mant"), self._gpu(name + ".exps"), int(K), int(N), fmt)
+
+  def vector(self, name):
+    return self._gpu(name).reshape(-1).contiguous()
+
+  def table(self, name="embed_tokens"):
+    return self._gpu(name).contiguous()

@@ -65,3 +65,29 @@ def test_refuses_tensors_it_cannot_apply(tmp_path, name):
                                                        name: np.zeros((16,), np.float32)})
   with pytest.raises(NotImplementedError, match="not on this path"):
     K.Checkpoint(str(tmp_path), device="cpu")
+
+
+def test_packed_file_round_trip(tmp_path):
+  # save_packed's file read back by Packed (on the CPU: any torch tensors): the matrices' bytes with their format and
+  # shape, the norms, the embedding; a file of another kind refused
+  import torch
+  from types import SimpleNamespace
+  from ferrite_amd import ops
+  rng = np.random.default_rng(46)
+  u8 = lambda n: torch.from_numpy(rng.integers(0, 256, n).astype(np.uint8))
+  mat = lambda K, N, fmt: ops.BfpWeight(u8(K * N // (1 if fmt == "bfp8" else 2)), u8(K * N // 16), K, N, fmt)
+  f32 = lambda n: torch.from_numpy(rng.normal(0, 1, n).astype(np.float32))
+  L = SimpleNamespace(qkv=mat(64, 96, "bfp8"), o=mat(32, 64, "bfp8"), gate_up=mat(64, 128, "bfp4"), down=mat(64, 64, "bfp4"),
+                      norm1=f32(64), norm2=f32(64))
+  dec = SimpleNamespace(mode="bfp4", layers=[L], norm=f32(64), embed=f32((10, 64)).to(torch.bfloat16), head=mat(64, 16, "bfp8"))
+  path = str(tmp_path / "p.safetensors")
+  K.save_packed(dec, path)
+  p = K.Packed(path, device="cpu")
+  for name, bw in (("layers.0.qkv_proj", L.qkv), ("layers.0.gate_up_proj", L.gate_up), ("embed.T", dec.head)):
+    got = p.pack(name, bw.fmt)
+    assert (got.K, got.N, got.fmt) == (bw.K, bw.N, bw.fmt) and torch.equal(got.mant, bw.mant) and torch.equal(got.exps, bw.exps)
+  with pytest.raises(ValueError): p.pack("layers.0.qkv_proj", "bfp4")
+  assert torch.equal(p.vector("layers.0.post_attention_layernorm"), L.norm2) and torch.equal(p.vector("norm"), dec.norm)
+  assert torch.equal(p.table(), dec.embed)
+  C.write_safetensors(tmp_path / "other.safetensors", {"x": np.zeros((2, 2), np.float32)})
+  with pytest.raises(ValueError): K.Packed(str(tmp_path / "other.safetensors"), device="cpu")

@@ -48,6 +48,25 @@ def test_decoder_from_checkpoint(cuda, tmp_path, tied):
     assert torch.equal(la, lb) and torch.isfinite(la).all(), i
 
 
+def test_packed_weights_file(cuda, tmp_path):
+  # a Decoder's packed weights saved once (save_packed) and loaded back (Packed) without the checkpoint or a repacking:
+  # the same bytes, so the same logits bit for bit; a precision that asks another format is refused
+  from ferrite_amd import checkpoint as K, llama as G
+  t = C.llama(tmp_path, np.random.default_rng(45), layers=2, tied=True)
+  c = K.config(str(tmp_path), places=64)
+  a = G.Decoder(c, K.Checkpoint(str(tmp_path)), mode="bfp4", kv="bf16", context=64)
+  path = str(tmp_path / "packed.safetensors")
+  K.save_packed(a, path)
+  b = G.Decoder(c, K.Packed(path), mode="bfp4", kv="bf16", context=64)
+  for L, M in zip(a.layers, b.layers):
+    for n in ("qkv", "o", "gate_up", "down"):
+      assert torch.equal(getattr(L, n).mant, getattr(M, n).mant) and torch.equal(getattr(L, n).exps, getattr(M, n).exps), n
+  assert torch.equal(a.head.mant, b.head.mant) and torch.equal(a.embed, b.embed) and torch.equal(a.norm, b.norm)
+  for i, tok in enumerate([5, 300, 17]):
+    assert torch.equal(a.step([tok], [i], replay=False)[0].cpu(), b.step([tok], [i], replay=False)[0].cpu()), i
+  with pytest.raises(ValueError): G.Decoder(c, K.Packed(path), mode="bfp8", kv="bf16", context=64)
+
+
 def test_mixtral_experts_from_rows(cuda, tmp_path):
   from ferrite_amd import checkpoint as K, ops
   t = C.llama(tmp_path, np.random.default_rng(44), layers=1, experts=4, ffn=128)
