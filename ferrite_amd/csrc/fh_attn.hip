@@ -232,33 +232,40 @@ __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(AttArgs a) {
 
 // The same chunk walk on the matrix cores, for a workgroup that takes several chunks (the throughput case: many rows)
 // of a bf16 or block-float cache: 4 waves, wave w the chunk's rows 16 w .. 16 w + 15 for every query head at once
-// (v_mfma_f32_16x16x32_bf16, heads as N). Scores S = K q^T: A the keys' rows from the LDS tile, B q in three bf16
-// terms that sum to it exactly (each the next 8 significant bits), so the products stay fp32-exact. The softmax
-// statistics of each head meet across the waves in LDS; p is written to LDS in three bf16 terms; O += p V with A
-// p's terms and B the values' columns read transposed (ds_read_b64_tr_b16), wave w a quarter of the dimensions.
+// (v_mfma_f32_16x16x32_bf16, heads as N). Scores S = K q^T: A the keys' rows from the LDS tile, B q in two bf16
+// terms (q to nearest, then the rest to nearest: their sum is q within 2^-16 |q|, and each product of bf16 values is
+// exact in fp32). The softmax statistics of each head meet across the waves in LDS; p is written to LDS in two bf16
+// terms the same way; O += p V with A p's terms and B the values' columns read transposed (ds_read_b64_tr_b16), wave w
+// a quarter of the dimensions. Two terms rather than three keep the workgroup within 40 KB of LDS and 128 registers a
+// lane, so that four of them fit a CU.
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 att_bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float att_floatx4;
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short att_short4;
 #define ATT_LDS __attribute__((address_space(3)))
 constexpr int ATT_PS = ATT_CHUNK + 8;  // a head's row of p in LDS, bf16 (144 bytes)
 
-// x as three floats with bf16 values whose sum is x exactly (truncations to 8 significant bits, then the rest's)
-__device__ inline void split3(float x, float& t1, float& t2, float& t3) {
-  t1 = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
-  const float r1 = x - t1;
-  t2 = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
-  t3 = r1 - t2;
+constexpr int ATT_T = 2;  // bf16 terms of q and of p
+
+__device__ inline float att_rne(float x) {  // x rounded to bf16 (nearest even), as a float
+  const uint32_t u = __float_as_uint(x);
+  return __uint_as_float((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
+}
+// x as two floats with bf16 values: x to nearest, then the rest (exact in fp32) to nearest; |x - t0 - t1| <= 2^-16 |x|
+__device__ inline void split2(float x, float (&t)[ATT_T]) {
+  t[0] = att_rne(x);
+  t[1] = att_rne(x - t[0]);
 }
 __device__ inline uint32_t pack_hi(float lo, float hi) {  // two floats with bf16 values: their high halves
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
 static size_t att_mfma_lds(int hd) {
-  return (size_t)2 * ATT_CHUNK * att_row_bytes(hd, 2) + (size_t)3 * 16 * ATT_PS * 2 + (size_t)(2 * 4 * 16 + 3 * 16) * 4;
+  return (size_t)2 * ATT_CHUNK * att_row_bytes(hd, 2) + (size_t)ATT_T * 16 * ATT_PS * 2 + (size_t)(2 * 4 * 16 + 3 * 16) * 4;
 }
 
 template <int HD, int CF>
-__global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))  // (4 workgroups a CU: 128 registers)
+void attention_mfma(AttArgs a) {
   using Loader = ChunkLoader<HD, CF>;
   constexpr int RW = Loader::RW, RWS = RW / 2;   // a tile row in bytes and in bf16s
   constexpr int KS = HD / 32;                    // K steps of the scores
@@ -275,8 +282,8 @@ __global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
   const int parts = nchunks < S ? nchunks : S;
   char* ks = att_smem;
   char* vs = att_smem + ATT_CHUNK * RW;
-  uint16_t* ps = (uint16_t*)(att_smem + 2 * ATT_CHUNK * RW);          // [3][16 heads][ATT_PS]
-  float* wmax_s = (float*)(ps + 3 * 16 * ATT_PS);                     // [4 waves][16 heads]
+  uint16_t* ps = (uint16_t*)(att_smem + 2 * ATT_CHUNK * RW);          // [ATT_T][16 heads][ATT_PS]
+  float* wmax_s = (float*)(ps + ATT_T * 16 * ATT_PS);                 // [4 waves][16 heads]
   float* wsum_s = wmax_s + 64;
   float* m_s = wsum_s + 64;                                           // [16] running max
   float* l_s = m_s + 16;                                              // [16] running sum
@@ -288,8 +295,8 @@ __global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
   Loader ld;
   ld.load(a, krow0 + (int64_t)split * ATT_CHUNK, vrow0 + (int64_t)split * ATT_CHUNK, rows_of(split), 0, tid, 256);
 
-  // q as B: lane's head c16 (zero past rep), dimensions 32 s + 8 g .. + 7, three terms
-  att_bf16x8 qb[KS][3];
+  // q as B: lane's head c16 (zero past rep), dimensions 32 s + 8 g .. + 7, ATT_T terms
+  att_bf16x8 qb[KS][ATT_T];
   {
     const bool hv = c16 < rep;
     const float* qh = a.q + ((int64_t)b * a.heads + (int64_t)kvh * rep + (hv ? c16 : 0)) * HD + 8 * g;
@@ -297,11 +304,11 @@ __global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
     for (int s = 0; s < KS; ++s) {
       const float4 u = *(const float4*)(qh + 32 * s), v = *(const float4*)(qh + 32 * s + 4);
       const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-      float t[3][8];
+      float t[ATT_T][8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) split3(hv ? x[i] : 0.f, t[0][i], t[1][i], t[2][i]);
+      for (int i = 0; i < 8; ++i) { float u[ATT_T]; split2(hv ? x[i] : 0.f, u); for (int j = 0; j < ATT_T; ++j) t[j][i] = u[j]; }
 #pragma unroll
-      for (int j = 0; j < 3; ++j) {
+      for (int j = 0; j < ATT_T; ++j) {
         const uint4 pk = make_uint4(pack_hi(t[j][0], t[j][1]), pack_hi(t[j][2], t[j][3]), pack_hi(t[j][4], t[j][5]), pack_hi(t[j][6], t[j][7]));
         qb[s][j] = *(const att_bf16x8*)&pk;
       }
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
     for (int s = 0; s < KS; ++s) {
       const att_bf16x8 ka = *(const att_bf16x8*)(ks + (16 * w + c16) * RW + (32 * s + 8 * g) * 2);
 #pragma unroll
-      for (int j = 0; j < 3; ++j) sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[s][j], sc, 0, 0, 0);
+      for (int j = 0; j < ATT_T; ++j) sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[s][j], sc, 0, 0, 0);
     }
     const bool hv = c16 < rep;
     float sv[4], wm = -INFINITY;
@@ -355,12 +362,12 @@ __global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
     wsum += __shfl_xor(wsum, 16, 64);
     wsum += __shfl_xor(wsum, 32, 64);
     if (g == 0) wsum_s[w * 16 + c16] = wsum;
-    {  // p's three terms: head c16, rows 16 w + 4 g .. + 3
-      float t[3][4];
+    {  // p's terms: head c16, rows 16 w + 4 g .. + 3
+      float t[ATT_T][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) split3(pv[i], t[0][i], t[1][i], t[2][i]);
+      for (int i = 0; i < 4; ++i) { float u[ATT_T]; split2(pv[i], u); for (int j = 0; j < ATT_T; ++j) t[j][i] = u[j]; }
 #pragma unroll
-      for (int j = 0; j < 3; ++j)
+      for (int j = 0; j < ATT_T; ++j)
         *(uint2*)(ps + (j * 16 + c16) * ATT_PS + 16 * w + 4 * g) = make_uint2(pack_hi(t[j][0], t[j][1]), pack_hi(t[j][2], t[j][3]));
     }
     __syncthreads();
@@ -384,9 +391,9 @@ __global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
       for (int i = 0; i < 4; ++i) acc_o[tt][i] *= fr[i];
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
-      att_bf16x8 pa[3];
+      att_bf16x8 pa[ATT_T];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) pa[j] = *(const att_bf16x8*)(ps + (j * 16 + c16) * ATT_PS + 32 * s2 + 8 * g);
+      for (int j = 0; j < ATT_T; ++j) pa[j] = *(const att_bf16x8*)(ps + (j * 16 + c16) * ATT_PS + 32 * s2 + 8 * g);
 #pragma unroll
       for (int tt = 0; tt < TPW; ++tt) {
         const int col = 16 * (w * TPW + tt);
@@ -395,7 +402,7 @@ __global__ __launch_bounds__(256) void attention_mfma(AttArgs a) {
         const short v8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         const att_bf16x8 vb = *(const att_bf16x8*)v8;
 #pragma unroll
-        for (int j = 0; j < 3; ++j) acc_o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[j], vb, acc_o[tt], 0, 0, 0);
+        for (int j = 0; j < ATT_T; ++j) acc_o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[j], vb, acc_o[tt], 0, 0, 0);
       }
     }
     __syncthreads();  // the tiles, p and the statistics are rewritten by the next chunk

@@ -231,7 +231,7 @@ def test_attention_decode(cuda, hd, heads, kv):
 @pytest.mark.parametrize("hd,heads,kv,batch,part", [(128, 32, 8, 16, 1000), (64, 9, 3, 64, 600)])
 def test_attention_decode_many_rows(cuda, hd, heads, kv, batch, part):
   # many rows x key heads: few enough workgroups that each walks several chunks of its row (online softmax across
-  # them; a bf16 or block-float cache takes the matrix cores, q and p in three bf16 terms each), rows shorter than the
+  # them; a bf16 or block-float cache takes the matrix cores, q and p in two bf16 terms each), rows shorter than the
   # workgroups sharing them, ending inside a chunk and at its edge; a block float's values read bit for bit as the
   # same values in a bf16 cache
   rng = np.random.default_rng(5 + hd)
