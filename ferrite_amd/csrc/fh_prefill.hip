@@ -90,6 +90,8 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
   const int64_t qplace = a.p0 + qr;
   const int64_t last_key = a.p0 + min(qt * PA_BQ + PA_BQ, a.T) - 1;  // the workgroup's last key (its last row's place)
   const int nkt = (int)(last_key / PA_BK) + 1;
+  // the wave's first row's place: a key tile wholly at or before it is visible to every row of the wave (no mask)
+  const int64_t wave_first = a.p0 + min(qt * PA_BQ + wave * 32, a.T - 1);
 
   // the lane's query, bf16, in the B-operand layout: step s holds dimensions 16 s + 8 hh .. + 7
   bf16x8 qf[HD / 16];
@@ -179,17 +181,28 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kb], 0, 0, 0);
       }
     }
-    // scale, mask past the query's place, and the online softmax
+    // scale, mask past the query's place (only on a tile reaching past the wave's first row), and the online softmax
     float mt = PA_MASKED;
+    if (k0 + PA_BK - 1 > wave_first) {
+      const int kq = (int)(qplace - k0);  // (the key's offset in the tile: visible up to this)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hh + (r & 3);
-        const float v = key <= qplace ? s[kb][r] * a.scale : PA_MASKED;
-        s[kb][r] = v;
-        mt = fmaxf(mt, v);
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int key = 32 * kb + 8 * (r >> 2) + 4 * hh + (r & 3);
+          const float v = key <= kq ? s[kb][r] * a.scale : PA_MASKED;
+          s[kb][r] = v;
+          mt = fmaxf(mt, v);
+        }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s[kb][r] *= a.scale;
+          mt = fmaxf(mt, s[kb][r]);
+        }
+    }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float mn = fmaxf(m, mt);
     const float alpha = __expf(m - mn);
