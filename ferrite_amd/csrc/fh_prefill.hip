@@ -92,6 +92,8 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
   const int nkt = (int)(last_key / PA_BK) + 1;
   // the wave's first row's place: a key tile wholly at or before it is visible to every row of the wave (no mask)
   const int64_t wave_first = a.p0 + min(qt * PA_BQ + wave * 32, a.T - 1);
+  // scores kept in base 2 (scale times log2 e): the softmax's exponentials are then the chip's exp2 alone
+  const float scale2 = a.scale * 1.44269504088896341f;
 
   // the lane's query, bf16, in the B-operand layout: step s holds dimensions 16 s + 8 hh .. + 7
   bf16x8 qf[HD / 16];
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = 32 * kb + 8 * (r >> 2) + 4 * hh + (r & 3);
-          const float v = key <= kq ? s[kb][r] * a.scale : PA_MASKED;
+          const float v = key <= kq ? s[kb][r] * scale2 : PA_MASKED;
           s[kb][r] = v;
           mt = fmaxf(mt, v);
         }
@@ -199,19 +201,19 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          s[kb][r] *= a.scale;
+          s[kb][r] *= scale2;
           mt = fmaxf(mt, s[kb][r]);
         }
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float mn = fmaxf(m, mt);
-    const float alpha = __expf(m - mn);
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);
     float rsum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = __expf(s[kb][r] - mn);
+        const float p = __builtin_amdgcn_exp2f(s[kb][r] - mn);
         s[kb][r] = p;
         rsum += p;
       }
