@@ -153,10 +153,10 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
         lo[j][0] = w.x; lo[j][1] = w.y; lo[j][2] = w.z; lo[j][3] = w.w;
       }
 #pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        const int sh = 16 * (d & 1), p = d >> 1;
-        const uint32_t k01 = ((lo[0][p] >> sh) & 0xFFFFu) | (((lo[1][p] >> sh) & 0xFFFFu) << 16);
-        const uint32_t k23 = ((lo[2][p] >> sh) & 0xFFFFu) | (((lo[3][p] >> sh) & 0xFFFFu) << 16);
+      for (int d = 0; d < 8; ++d) {  // (a byte permute a word: dimension d's halves of two keys' words)
+        const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u, p = d >> 1;
+        const uint32_t k01 = __builtin_amdgcn_perm(lo[1][p], lo[0][p], sel);
+        const uint32_t k23 = __builtin_amdgcn_perm(lo[3][p], lo[2][p], sel);
         *(uint2*)(Vt + (8 * dg + d) * VLD + 4 * kq) = make_uint2(k01, k23);
       }
     }
