@@ -135,7 +135,10 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
       for (int j = 0; j < 4; ++j) vraw[j] = cache_raw<HD, CF>(a, vrow + min(k0 + 4 * kq + j, last_key), 8 * dg);
     }
   };
-  // a tile's loads, as bf16, into buffer b: K rows; V^T, a thread's 4 keys x 8 dimensions as 8 rows of 4 keys
+  // a tile's loads, as bf16, into buffer b: K rows; V^T, a thread's 4 keys x 8 dimensions as 8 rows of 4 keys. In a
+  // V^T row each 16 keys lie as 0-3, 8-11, 4-7, 12-15, so that the 8 keys a lane multiplies at a 16-key step (4 hh ..
+  // 4 hh + 3 and 8 + 4 hh .. 8 + 4 hh + 3, the score layout's) are one 16-byte read
+  auto vt_col = [](int kq) { return 16 * (kq >> 2) + 4 * (((kq & 1) << 1) | ((kq >> 1) & 1)); };
   auto store_tile = [&](int b) {
     uint16_t* Ks = Ks2[b];
     uint16_t* Vt = Vt2[b];
@@ -157,7 +160,7 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
         const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u, p = d >> 1;
         const uint32_t k01 = __builtin_amdgcn_perm(lo[1][p], lo[0][p], sel);
         const uint32_t k23 = __builtin_amdgcn_perm(lo[3][p], lo[2][p], sel);
-        *(uint2*)(Vt + (8 * dg + d) * VLD + 4 * kq) = make_uint2(k01, k23);
+        *(uint2*)(Vt + (8 * dg + d) * VLD + vt_col(kq)) = make_uint2(k01, k23);
       }
     }
   };
@@ -236,9 +239,7 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
         const int g = 32 * kb + 16 * j;
 #pragma unroll
         for (int d = 0; d < HD / 32; ++d) {
-          const uint16_t* row = Vt + (32 * d + ql) * VLD + g;
-          const uint2 v0 = *(const uint2*)(row + 4 * hh), v1 = *(const uint2*)(row + 8 + 4 * hh);
-          const uint4 vv = make_uint4(v0.x, v0.y, v1.x, v1.y);
+          const uint4 vv = *(const uint4*)(Vt + (32 * d + ql) * VLD + g + 8 * hh);
           acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)&vv, pf, acc[d], 0, 0, 0);
         }
       }
