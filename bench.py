@@ -2,7 +2,7 @@
 attention and the output layer in bfp8, every MLP matrix in bfp4, a bf16 KV cache at context 2048, batch 1).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c3-bfp8|c2] [--batch B] [--no-cpu] [--no-prefill]
-                [--only bs16|prefill|moe|floor]
+                [--only bs16|prefill|moe|floor|peaks]
 
 Prints ONE JSON line: tokens/s of the whole decode step (every kernel of it replayed as one HIP graph, inputs resident
 in HBM), the dominant GEMV's achieved HBM bandwidth against the 8 TB/s peak (timed live with HIP events on its own
@@ -12,7 +12,8 @@ its own field, with the same step with every matrix bfp8 (`decode_bfp8`), batche
 `configs` holds config 1's GEMV and config 2's SmolLM step on the GPU, and the numpy CPU baselines of configs 1, 2, 4
 and 5 (bounded samples, each saying how it was scaled). Synthetic data: random-init weights, drawn on the GPU and
 packed there. --only runs one part by itself and prints its fields as the JSON line (what a profiler run of one part
-uses): the batch-16 step, config 4's prefill, config 5's MoE layer, or the read floor (read_floor)."""
+uses): the batch-16 step, config 4's prefill, config 5's MoE layer, the read floor (read_floor), or the matrix
+cores' and LDS's own rates (core_peaks)."""
 import argparse, json, os, statistics, sys, time
 import numpy as np
 import torch
@@ -362,6 +363,38 @@ def measured_traffic(kernel, config, batch):
   return None
 
 
+def core_peaks(dev, reps=5):
+  """What the matrix cores and LDS reach on this GPU with nothing else to do (fh_mfma_probe, fh_lds_probe): MFMA loops
+  of each form over 1024 and 2048 workgroups of 4 waves (16 and 32 waves a CU), 8 independent accumulators a wave;
+  16-byte LDS reads over 2048 workgroups of 256 threads (8 a CU, 16 KiB of LDS each). Timed by HIP events on the
+  current stream after a warm-up, the best of the grids; the LDS rate also per CU and clock at the 2.4 GHz peak engine
+  clock."""
+  from ferrite_amd import lib
+  s = torch.cuda.current_stream().cuda_stream
+  sink = torch.empty(2048, dtype=torch.float32, device=dev)
+  def timed(fn):
+    fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps): fn()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / reps * 1e-3
+  out = {}
+  for form, name, flops in ((0, "mfma_32x32x16_bf16_tflops", 32768), (1, "mfma_16x16x32_bf16_tflops", 16384)):
+    iters = 200
+    out[name] = round(max(blocks * 4 * iters * 8 * flops / timed(lambda: lib.call("fh_mfma_probe", form, iters, sink.data_ptr(), blocks, s))
+                          for blocks in (1024, 2048)) / 1e12, 1)
+  iters, blocks = 2000, 2048
+  t = timed(lambda: lib.call("fh_lds_probe", iters, sink.data_ptr(), blocks, s))
+  rate = blocks * 256 * iters * 4 * 16 / t
+  cus = torch.cuda.get_device_properties(dev).multi_processor_count
+  out["lds_read_tbs"] = round(rate / 1e12, 1)
+  out["lds_read_bytes_per_clk_cu"] = round(rate / cus / 2.4e9, 1)
+  return out
+
+
 def read_floor(dev, reps=5):
   """What a plain read of each batch-1 GEMV's bytes takes, launched as the step launches a GEMV: a graph of 32 launches
   back to back over 32 distinct buffers (each read from HBM), each launch fh_read_probe (16-byte loads, four in flight
@@ -479,7 +512,7 @@ def main():
   ap.add_argument("--batch", type=int, default=1)
   ap.add_argument("--no-cpu", action="store_true")
   ap.add_argument("--no-prefill", action="store_true", help="skip config 4's prefill measurement")
-  ap.add_argument("--only", choices=("bs16", "prefill", "moe", "floor"), help="run one part alone (see above)")
+  ap.add_argument("--only", choices=("bs16", "prefill", "moe", "floor", "peaks"), help="run one part alone (see above)")
   ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                   help="first run a plain copy kernel (torch.neg) over MIB MiB: the known-size kernel that calibrates "
                        "rocprofv3's FETCH_SIZE/WRITE_SIZE counters in the same run")
@@ -505,6 +538,7 @@ def main():
       r = decode_batch(dec, context)
     elif args.only == "prefill": r = prefill_rate()
     elif args.only == "moe": r = {"moe": moe_rate(), "moe_prompt": moe_rate(2048, reps=5)}
+    elif args.only == "peaks": r = core_peaks(dev)
     else: r = read_floor(dev)
     print(json.dumps({"only": args.only, **r}), flush=True)
     return

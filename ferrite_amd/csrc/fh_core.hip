@@ -305,6 +305,79 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const uint4* src, int64
   if (threadIdx.x == 0) sink[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
 }
 
+// The matrix cores' own rate: each wave `iters` rounds of 8 independent accumulators, one MFMA each (32x32x16 bf16,
+// form 0, or 16x16x32, form 1), operands from registers; each workgroup's sum of its results to sink[block]
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 probe_bf16x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float probe_floatx16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float probe_floatx4;
+template <int FORM>
+__global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, float* sink) {
+  probe_bf16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { a[i] = (__bf16)(float)((threadIdx.x + i) & 7); b[i] = (__bf16)(float)((threadIdx.x * 3 + i) & 7); }
+  float total = 0.f;
+  if constexpr (FORM == 0) {
+    probe_floatx16 acc[8] = {};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) total += acc[j][r];
+  } else {
+    probe_floatx4 acc[8] = {};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) total += acc[j][r];
+  }
+  total = wave_sum(total);
+  __shared__ float part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = total;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = part[0] + part[1] + part[2] + part[3];
+}
+
+// LDS read rate: each thread `iters` rounds of four 16-byte reads of a 16 KiB buffer at addresses that rotate with the
+// round (every 16 lanes on distinct banks); each workgroup's xor of what it read to sink[block]
+__global__ __launch_bounds__(256) void lds_probe_kernel(int iters, uint32_t* sink) {
+  __shared__ __attribute__((aligned(16))) uint4 buf[1024];
+  for (int i = threadIdx.x; i < 1024; i += 256) buf[i] = make_uint4(i, i * 3u, i * 5u, i * 7u);
+  __syncthreads();
+  uint32_t x = 0;
+#pragma clang loop unroll(disable)
+  for (int it = 0; it < iters; ++it) {  // (not unrolled: no round's reads can stand in for another's)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint4 v = buf[(threadIdx.x + 256 * u + 64 * it) & 1023];
+      x ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+  }
+  for (int m = 32; m >= 1; m >>= 1) x ^= (uint32_t)__shfl_xor((int)x, m, 64);
+  __shared__ uint32_t part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+}
+
+extern "C" int fh_mfma_probe(int form, int iters, float* sink, int blocks, void* stream) {
+  if (!sink || (form != 0 && form != 1) || iters < 1 || blocks < 1 || blocks > 65536)
+    return fail(FH_EINVAL, "fh_mfma_probe: need sink, form 0 or 1, iters >= 1 and 1..65536 blocks");
+  if (form == 0) hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(blocks), dim3(256), 0, as_stream(stream), iters, sink);
+  else hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(blocks), dim3(256), 0, as_stream(stream), iters, sink);
+  return check_launch("fh_mfma_probe");
+}
+
+extern "C" int fh_lds_probe(int iters, uint32_t* sink, int blocks, void* stream) {
+  if (!sink || iters < 1 || blocks < 1 || blocks > 65536) return fail(FH_EINVAL, "fh_lds_probe: need sink, iters >= 1 and 1..65536 blocks");
+  hipLaunchKernelGGL(lds_probe_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), iters, sink);
+  return check_launch("fh_lds_probe");
+}
+
 extern "C" int fh_read_probe(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream) {
   if (!src || !sink || bytes < 16 || bytes % 16 || blocks < 1 || blocks > 65536)
     return fail(FH_EINVAL, "fh_read_probe: need src, sink, bytes a multiple of 16 and 1..65536 blocks");

@@ -66,6 +66,8 @@ SIGNATURES = {
   "fh_argmax_rows": ([P, L, L, P, P], I),
   "fh_argmax_parts": ([P, L, L, P, P], I),
   "fh_read_probe": ([P, S, P, I, P], I),
+  "fh_mfma_probe": ([I, I, P, I, P], I),
+  "fh_lds_probe": ([I, P, I, P], I),
   "fh_heads_workspace_bytes": ([I, L, I], S),
   "fh_logit_heads": ([P, L, I, L, I, P, P, P, P, P, S, P], I),
   "fh_gather_cols": ([P, L, L, P, L, L, L, P, L, P], I),

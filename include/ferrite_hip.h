@@ -361,6 +361,13 @@ int fh_put_rows(void* dst, int64_t dst_rows, int64_t dst_ld, int64_t dst_plane, 
  * src read once by `blocks` workgroups of 256 threads, 16 bytes a load and four loads in flight a thread, each
  * workgroup's xor of the 32-bit words it read into sink[block] ([blocks] uint32). No counterpart in the reference. */
 int fh_read_probe(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream);
+/* The matrix cores' own rate (bench.py's peaks): `blocks` workgroups of 4 waves, each wave `iters` rounds of 8
+ * independent v_mfma_f32_32x32x16_bf16 (form 0; 32,768 FLOPs each) or v_mfma_f32_16x16x32_bf16 (form 1; 16,384),
+ * operands in registers; each workgroup's sum of its results into sink[block] ([blocks] float). And the LDS read rate:
+ * each of 256 threads a workgroup `iters` rounds of four 16-byte reads of a 16 KiB buffer, every 16 lanes on distinct
+ * banks; each workgroup's xor into sink[block] ([blocks] uint32). No counterpart in the reference. */
+int fh_mfma_probe(int form, int iters, float* sink, int blocks, void* stream);
+int fh_lds_probe(int iters, uint32_t* sink, int blocks, void* stream);
 
 #ifdef __cplusplus
 }
