@@ -296,6 +296,8 @@ void attention_mfma(AttArgs a) {
   ld.load(a, krow0 + (int64_t)split * ATT_CHUNK, vrow0 + (int64_t)split * ATT_CHUNK, rows_of(split), 0, tid, 256);
 
   // q as B: lane's head c16 (zero past rep), dimensions 32 s + 8 g .. + 7, ATT_T terms
+  // scores kept in base 2 (scale times log2 e): each exponential the chip's exp2 alone
+  const float scale2 = a.scale * 1.44269504088896341f;
   att_bf16x8 qb[KS][ATT_T];
   {
     const bool hv = c16 < rep;
@@ -346,7 +348,7 @@ void attention_mfma(AttArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool ok = hv && 16 * w + 4 * g + i < n;
-      sv[i] = ok ? sc[i] * a.scale : -INFINITY;
+      sv[i] = ok ? sc[i] * scale2 : -INFINITY;
       wm = fmaxf(wm, sv[i]);
     }
     wm = fmaxf(wm, __shfl_xor(wm, 16, 64));
@@ -358,7 +360,7 @@ void attention_mfma(AttArgs a) {
     for (int v = 0; v < 4; ++v) mn = fmaxf(mn, wmax_s[v * 16 + c16]);
     float pv[4], wsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { pv[i] = sv[i] == -INFINITY ? 0.f : expf(sv[i] - mn); wsum += pv[i]; }
+    for (int i = 0; i < 4; ++i) { pv[i] = sv[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[i] - mn); wsum += pv[i]; }
     wsum += __shfl_xor(wsum, 16, 64);
     wsum += __shfl_xor(wsum, 32, 64);
     if (g == 0) wsum_s[w * 16 + c16] = wsum;
@@ -375,7 +377,7 @@ void attention_mfma(AttArgs a) {
       float mh = m_s[tid], sum = 0.f;
 #pragma unroll
       for (int v = 0; v < 4; ++v) { mh = fmaxf(mh, wmax_s[v * 16 + tid]); sum += wsum_s[v * 16 + tid]; }
-      const float f = tid < rep && mh != -INFINITY ? expf(m_s[tid] - mh) : 0.f;  // (0 on the first chunk)
+      const float f = tid < rep && mh != -INFINITY ? __builtin_amdgcn_exp2f(m_s[tid] - mh) : 0.f;  // (0 on the first chunk)
       l_s[tid] = fmaf(l_s[tid], f, sum);
       m_s[tid] = mh;
       f_s[tid] = f;
@@ -421,7 +423,7 @@ void attention_mfma(AttArgs a) {
       float* pp = a.part + (((int64_t)b * a.heads + h) * S + split) * (HD + 2);
 #pragma unroll
       for (int tt = 0; tt < TPW; ++tt) pp[16 * (w * TPW + tt) + c16] = acc_o[tt][i];
-      if (w == 0 && c16 == 0) { pp[HD] = m_s[hh]; pp[HD + 1] = l_s[hh]; }
+      if (w == 0 && c16 == 0) { pp[HD] = m_s[hh] * 0.693147180559945309f; pp[HD + 1] = l_s[hh]; }  // (the max in e's base)
     }
   }
 }
