@@ -152,8 +152,11 @@ class Decoder:
     self.q, self.att = z(B, c.heads * hd), z(B, c.heads * hd)
     self.h = z(B, c.ffn)
     # the matrix cores' bf16 rows: each residual epilogue's copy, SwiGLU's output, attention's output for o; in tiles of
-    # 16 rows (FH_BF16_T16) up to 64 rows, which the matrix-core kernel for a few rows loads a whole line at a time
-    rows16 = ops.tiles16 if B <= 64 else (lambda r, n, d: torch.zeros(r, n, dtype=torch.bfloat16, device=d))
+    # 16 rows (FH_BF16_T16) up to 64 rows, which the matrix-core kernel for a few rows loads a whole line at a time. That
+    # kernel takes K a multiple of 64 only: a model with any matmul's K (dim, heads head_dim, ffn) off that keeps plain
+    # bf16 rows, which the tiled GEMM takes at any K
+    tiled = B <= 64 and all(k % 64 == 0 for k in (c.dim, c.heads * hd, c.ffn))
+    rows16 = ops.tiles16 if tiled else (lambda r, n, d: torch.zeros(r, n, dtype=torch.bfloat16, device=d))
     self.xn = rows16(B, c.dim, self.device)
     self.hb = rows16(B, c.ffn, self.device)
     self.attb = rows16(B, c.heads * hd, self.device)

@@ -47,16 +47,19 @@ class Runtime:
     self.stream = torch.cuda.Stream(device=self.device) if self.device.type == "cuda" else None
     self.launches = 0  # kernels launched (how many a realize took)
     self.queued = collections.deque()  # (launch, name, end event) of the launches that may not be done
-    self.times = {}  # launch % TIMES -> (launch, name, start event, end event)
+    self.times = {}  # launch % TIMES -> (launch, name, start event, end event, bytes read or None)
 
   def on(self):
     """A context with this runtime's stream current: torch allocations and copies inside it are ordered with its
     launches."""
     return torch.cuda.stream(self.stream) if self.stream is not None else contextlib.nullcontext()
 
-  def run(self, fn, name="launch"):
+  def run(self, fn, name="launch", nbytes=None):
     """fn() with this runtime's stream current (its library calls go on it), as launch number self.launches + 1 named
-    `name`; outside a graph capture it is bracketed by events, which wait() polls and profile() reads."""
+    `name`, reading `nbytes` bytes of device memory (the algorithmic bytes of its operands, each once; None if not
+    counted); outside a graph capture it is bracketed by events, which wait() polls and profile() reads. The launches
+    already done leave the queue here too (its head polled), so a loop of launches with no wait() keeps at most the
+    unfinished ones and TIMES more."""
     self.launches += 1
     if self.stream is None: return fn()
     with torch.cuda.stream(self.stream):
@@ -66,8 +69,9 @@ class Runtime:
       out = fn()
       end = torch.cuda.Event(enable_timing=True)
       end.record(self.stream)
-    self.times[self.launches % self.TIMES] = (self.launches, name, start, end)
+    self.times[self.launches % self.TIMES] = (self.launches, name, start, end, nbytes)
     self.queued.append((self.launches, name, end))
+    while len(self.queued) > self.TIMES and self.queued[0][2].query(): self.queued.popleft()
     return out
 
   def wait(self, timeout=60):
@@ -87,21 +91,23 @@ class Runtime:
       time.sleep(0.0002)
 
   def profile(self, since):
-    """The launches after launch number `since` by name, once they are done: [(name, launches, microseconds, None)],
+    """The launches after launch number `since` by name, once they are done: [(name, launches, microseconds, bytes)],
     the most time first (Runtime.profile, ferrite/runtime.py:416-428). A launch's time runs between events recorded on
-    the stream before and after it; bytes read are not counted here (None). Only the last TIMES launches are kept, and
-    those replayed from a recording carry no events."""
+    the stream before and after it; its bytes are what the host counted for it (run's nbytes: each operand read once,
+    a block float's packed bytes), summed by name, None where a launch of that name was not counted. Only the last
+    TIMES launches are kept, and those replayed from a recording carry no events."""
     self.wait()
     assert self.launches - since <= self.TIMES, f"{self.launches - since} launches to profile, the last {self.TIMES} kept"
     totals = {}
     for n in range(since + 1, self.launches + 1):
       rec = self.times.get(n % self.TIMES)
       if rec is None or rec[0] != n: continue
-      _, name, start, end = rec
-      t = totals.setdefault(name, [0, 0.0])
+      _, name, start, end, nbytes = rec
+      t = totals.setdefault(name, [0, 0.0, 0])
       t[0] += 1
       t[1] += start.elapsed_time(end) * 1000.0
-    return sorted(((name, k, us, None) for name, (k, us) in totals.items()), key=lambda r: -r[2])
+      t[2] = None if t[2] is None or nbytes is None else t[2] + nbytes
+    return sorted(((name, k, us, b) for name, (k, us, b) in totals.items()), key=lambda r: -r[2])
 
 
 class Tensor:
@@ -602,7 +608,8 @@ class Tensor:
       prog, inputs = _fit_program(self, self.shape, allow_acc=False)  # (a stored tensor: one copy op)
       p = _cprogram(prog, inputs)
       out, ld = into.data, into.data.stride()
-      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[into.dtype], *into.shape, ld[0], ld[1], ops._stream()), "map")
+      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[into.dtype], *into.shape, ld[0], ld[1], ops._stream()), "map",
+                  _read_bytes(inputs, into.shape))
       return into
     if self.data is not None: return self
     if self.op is None:  # made empty (ferrite's Tensor(rt, rows, cols, batch, dtype), the model's `empty`): its memory now
@@ -618,7 +625,7 @@ class Tensor:
       with self.rt.on(): out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
       p = _cprogram(prog, inputs)
       self.rt.run(lambda: lib.call("fh_softmax_rows", ctypes.byref(p), int(self.op == "log_softmax"), *src.shape, ops._ptr(out),
-                                   DT[self.dtype], ops._stream()), "softmax")
+                                   DT[self.dtype], ops._stream()), "softmax", _read_bytes(inputs, src.shape))
       self._done(out)
       return self
     if self.op in REDUCE:
@@ -628,7 +635,7 @@ class Tensor:
       with self.rt.on(): out = torch.empty(self.shape, dtype=TORCH[self.dtype], device=self.rt.device)
       p = _cprogram(prog, inputs)
       self.rt.run(lambda: lib.call("fh_reduce", ctypes.byref(p), lib.REDUCE_MAX if f == "max" else lib.REDUCE_SUM, axis,
-                                   *src.shape, ops._ptr(out), DT[self.dtype], ops._stream()), "reduce")
+                                   *src.shape, ops._ptr(out), DT[self.dtype], ops._stream()), "reduce", _read_bytes(inputs, src.shape))
       self._done(out)
       return self
     prog, inputs = _fit_program(self, self.shape, allow_acc=True)
@@ -639,7 +646,8 @@ class Tensor:
       mm._acc = False
       a, b = (u.realize() for u in mm.srcs)
       a, b = ((u if u.data.stride(2) == 1 else (u + 0).realize()) for u in (a, b))
-      self.rt.run(lambda: ops.matmul(a.data, b.data, p, out=out), "matmul")
+      self.rt.run(lambda: ops.matmul(a.data, b.data, p, out=out), "matmul",
+                  _tensor_bytes(a) + _tensor_bytes(b) + _read_bytes([i for i in inputs if i[0] is not mm], self.shape))
     elif mm is not None:
       mm._acc = False
       a, w = mm.srcs[0].realize(), mm.srcs[1].data
@@ -650,14 +658,16 @@ class Tensor:
       ep = ops.epilogue(lib.EP_PROGRAM)
       ep.program = ctypes.pointer(p)
       ep.keep.append(program)
+      nb = w.nbytes + _read_bytes([i for i in inputs if i[0] is not mm], self.shape)
       if w.K % 32 or (a.dtype == "fp32" and a.rows <= 8):  # fp32 rows, or a K the matrix cores do not take: the
         if x.dtype != torch.float32: x = a.float().realize().data[0]  # exact-product GEMV
-        self.rt.run(lambda: ops.gemv(x, w, ep, out=y), "matmul")
+        self.rt.run(lambda: ops.gemv(x, w, ep, out=y), "matmul", nb + x.numel() * x.element_size())
       else:  # the matrix cores (bf16 rows go in as they are: their products are exact too)
-        self.rt.run(lambda: ops.gemm(x, w, ep, out=y), "matmul")
+        self.rt.run(lambda: ops.gemm(x, w, ep, out=y), "matmul", nb + x.numel() * x.element_size())
     else:
       ld = out.stride()
-      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[self.dtype], *self.shape, ld[0], ld[1], ops._stream()), "map")
+      self.rt.run(lambda: lib.call("fh_map", ctypes.byref(p), ops._ptr(out), DT[self.dtype], *self.shape, ld[0], ld[1], ops._stream()), "map",
+                  _read_bytes(inputs, self.shape))
     self._done(out)
     return self
 
@@ -844,3 +854,18 @@ def _cprogram(prog, inputs):
     for j in range(3): p.in_stride[k][j] = st[j]
   p.keep = [t.data for t, _ in inputs]
   return p
+
+
+def _read_bytes(inputs, shape):
+  """The bytes a program over `shape` reads from its inputs, each element once: an input's elements along the axes it
+  does not broadcast (a stride of 0 reads one element for all of that axis)."""
+  n = 0
+  for t, st in inputs:
+    n += math.prod(d for d, s in zip(shape, st) if s != 0) * ITEMSIZE[t.dtype]
+  return n
+
+
+def _tensor_bytes(t):
+  """A realized tensor's bytes (a block float's packed bytes)."""
+  if isinstance(t.data, ops.BfpWeight): return t.data.nbytes
+  return sum(w.nbytes for w in t.data) if isinstance(t.data, (list, tuple)) else t.data.numel() * t.data.element_size()

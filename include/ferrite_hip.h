@@ -219,7 +219,9 @@ int fh_attention_decode(const float* q, const void* cache, int cache_dtype, int6
  * fh_attention_workspace_bytes(batch, heads, head_dim, max_context) exceeds that returns FH_EINVAL (an 8B model's 32
  * heads at context 2048 fit up to batch 16). Every call on one GPU shares that GPU's array: calls in order on one
  * stream are safe, calls that overlap on one GPU (several streams or threads at once) race. The array needs no
- * clearing (no call reads what it did not write). The stream's device must be the current device. */
+ * clearing (no call reads what it did not write). The stream's device must be the current device. The first call on
+ * a GPU looks up the array's address there (hipGetSymbolAddress, no allocation): a caller that captures calls into a
+ * HIP graph makes one call on that GPU before its capture, and the captured calls then replay as any other kernel. */
 #define FH_ATTENTION_SCRATCH_BYTES (16u << 20)
 int fh_attention_decode_noalloc(const float* q, const void* cache, int cache_dtype, int64_t cache_len, int batch,
                                 int heads, int kv_heads, int head_dim, const int32_t* places, const int32_t* first_row,

@@ -150,8 +150,8 @@ def attention(h, p, c, tables, mask, cache, rows):
   heads = split(qkv, nh)
   kv = heads[c.heads:]
   fmt = (c.precision or {}).get(("kv", None), ("bf16", None))[0]
-  if fmt in ("bfp8", "bfp4"): kv = bfp(kv, fmt)  # (llama.py:127-128: numpy rounds a block-float cache as the chip does)
-  elif fmt == "bf16" and getattr(c, "kv_rounded", False): kv = bf16(kv)  # a bf16 cache as a GPU (or the chip) keeps it; llama.py's doesn't
+  if fmt in ("bfp8", "bfp4"): kv = bfp(kv, fmt)  # (llama.py:127-128: numpy rounds a block-float cache as the chip does,
+                                                 # and keeps a bf16 one's values unrounded)
   cache[:, list(rows)] = kv
   q, k, v = heads[:c.heads], cache[:c.kv], cache[c.kv:]
   m = mask.shape[-1]
@@ -242,7 +242,6 @@ def forward_slots(ids, places, w, c, caches):
     for b, place in enumerate(places):
       kv = heads[c.heads:, b:b + 1]
       if fmt in ("bfp8", "bfp4"): kv = bfp(kv, fmt)
-      elif fmt == "bf16" and getattr(c, "kv_rounded", False): kv = bf16(kv)
       cache = caches[b][l]
       cache[:, [place]] = kv
       k, v = np.repeat(cache[:c.kv], rep, 0), np.repeat(cache[c.kv:], rep, 0)

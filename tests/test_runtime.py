@@ -19,10 +19,10 @@ def runtime():
   return rt
 
 
-def queue(rt, name, end, start=None):
+def queue(rt, name, end, start=None, nbytes=None):
   rt.launches += 1
   rt.queued.append((rt.launches, name, end))
-  rt.times[rt.launches % rt.TIMES] = (rt.launches, name, start or Event(0, 0.0), end)
+  rt.times[rt.launches % rt.TIMES] = (rt.launches, name, start or Event(0, 0.0), end, nbytes)
 
 
 def test_wait_times_out_naming_the_launch():
@@ -54,3 +54,40 @@ def test_profile_by_name():
   queue(rt, "matmul", Event(0, 12.0), Event(0, 11.0))   # 1 ms
   got = rt.profile(since)
   assert [(n, k, round(us)) for n, k, us, b in got] == [("matmul", 2, 5000), ("map", 1, 500)] and all(b is None for *_, b in got)
+
+
+def test_profile_bytes_by_name():
+  # each launch's counted bytes summed by name (ferrite's profile reports bytes read a name); a name with a launch the
+  # host did not count reports None
+  rt = runtime()
+  since = rt.launches
+  queue(rt, "matmul", Event(0, 4.0), Event(0, 1.0), nbytes=1000)
+  queue(rt, "matmul", Event(0, 8.0), Event(0, 6.0), nbytes=24)
+  queue(rt, "map", Event(0, 1.5), Event(0, 1.0), nbytes=8)
+  queue(rt, "map", Event(0, 2.5), Event(0, 2.0))
+  got = {n: (k, b) for n, k, us, b in rt.profile(since)}
+  assert got == {"matmul": (2, 1024), "map": (2, None)}
+
+
+def test_queue_drains_without_wait():
+  # launches already done leave the queue as new ones come: a loop of launches with no wait() keeps a bounded queue
+  rt = runtime()
+  for i in range(rt.TIMES + 50): queue(rt, "map", Event(0))
+  assert len(rt.queued) == rt.TIMES + 50  # (queue() is the bookkeeping alone; run()'s drain is what is checked next)
+  class Stream:
+    def query(self): return True
+  rt.stream = Stream()
+  import torch
+  real = torch.cuda.stream, torch.cuda.is_current_stream_capturing, torch.cuda.Event
+  class Ev:
+    def __init__(self, **k): pass
+    def record(self, s): pass
+    def query(self): return True
+  try:
+    torch.cuda.stream = lambda s: __import__("contextlib").nullcontext()
+    torch.cuda.is_current_stream_capturing = lambda: False
+    torch.cuda.Event = Ev
+    rt.run(lambda: None, "map", 8)
+  finally:
+    torch.cuda.stream, torch.cuda.is_current_stream_capturing, torch.cuda.Event = real
+  assert len(rt.queued) == rt.TIMES

@@ -61,3 +61,30 @@ def test_noalloc_refuses_past_its_scratch(cuda):
   with pytest.raises(ValueError, match="FH_ATTENTION_SCRATCH_BYTES"):
     lib.call("fh_attention_decode_noalloc", dummy, dummy, lib.BF16, 32 * 2048, 32, 32, 8, 128, dummy, dummy, 2048, dummy,
              lib.F32, None)
+
+
+def test_noalloc_under_graph_capture(cuda):
+  # the callers it is for: code under HIP graph capture. One call captured (torch.cuda.graph, on its side stream) and
+  # replayed three times, with eager work on the same scratch between the replays (a call of another shape), each
+  # replay's bits those of the workspace entry point. (The device's scratch address is looked up by the first call on
+  # that device, made here outside the capture, as a caller warming up before capture does.)
+  from ferrite_amd import lib, ops
+  rng = np.random.default_rng(98)
+  batch, heads, kv, hd, ctx = 16, 32, 8, 128, 2048
+  q, cache, places, first = case(rng, batch, heads, kv, hd, ctx, "bf16")
+  want, warm = call_both(lib, ops, q, cache, heads, kv, hd, places, first, ctx, torch.float32)
+  assert torch.equal(want, warm)
+  data, dtype, length = ops.cache_fields(cache)
+  o = torch.full(q.shape, float("nan"), dtype=torch.float32, device="cuda")
+  common = (ops._ptr(q), ops._ptr(data), dtype, length, batch, heads, kv, hd, ops._ptr(places), ops._ptr(first), ctx)
+  g = torch.cuda.CUDAGraph()
+  with torch.cuda.graph(g):
+    lib.call("fh_attention_decode_noalloc", *common, ops._ptr(o), lib.F32, ops._stream())
+  q2, cache2, places2, first2 = case(rng, 3, 9, 3, 64, 300, "fp32")
+  for r in range(3):
+    o.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    print(f"noalloc under capture: replay {r}", flush=True)
+    assert torch.equal(o, want), (r, float((o - want).abs().max()))
+    call_both(lib, ops, q2, cache2, 9, 3, 64, places2, first2, 300, torch.float32)  # (eager work on the scratch)
