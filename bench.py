@@ -228,29 +228,32 @@ def moe_rate(T=32, reps=20):
 
 
 def config1_rate(dev, copies=300, reps=10):
-  """Config 1: the bfp8 GEMV x[1,576] @ W[576,1536] (fh_gemv_bfp, fp32 out). Over `copies` distinct packed weights
+  """Config 1: the bfp8 GEMV x[1,576] @ W[576,1536] (fp32 out), its 16-element blocks along N (ferrite's own layout,
+  fh_gemv_bfp) and, as config 1's text states it, along K (fh_gemv_bfp_k). Over `copies` distinct packed weights
   (940,032 bytes each: 282 MB, past the 256 MB Infinity Cache) launched back to back in a HIP graph, so each launch
   reads its weight from HBM; and the same weight replayed (cache-resident: the launch's latency). Bytes a launch: the
   packed weight, x (bf16 values held in fp32, 576 x 4) and y (1536 x 4): 947,328 algorithmic bytes as config 1 counts
   them with x in bf16 (x is 2,304 bytes here, read as fp32)."""
-  from ferrite_amd import ops
+  from ferrite_amd import lib, ops
   K, N = 576, 1536
-  g = torch.Generator(device=dev)
-  g.manual_seed(11)
-  ws = [ops.pack(torch.randn(K, N, generator=g, device=dev) * 0.02, "bfp8") for _ in range(copies)]
-  x = torch.randn(1, K, generator=g, device=dev).to(torch.bfloat16).float()
-  y = torch.empty(1, N, device=dev)
-  stream = torch.cuda.Stream(device=dev)
-  def many():
-    for w in ws: ops.gemv(x, w, out=y)
-  ms = timed_graph(many, reps, stream) / copies
-  one = timed_graph(lambda: [ops.gemv(x, ws[0], out=y) for _ in range(copies)], reps, stream) / copies
   nbytes = K * N * 17 // 16 + K * 2 + N * 4
-  del ws
-  torch.cuda.empty_cache()
-  return {"workload": "config 1: bfp8 GEMV x[1,576] @ W[576,1536], fp32 out", "us": round(ms * 1e3, 3),
-          "gbs": round(nbytes / ms / 1e6, 1), "bytes": nbytes, "copies": copies,
-          "us_cache_resident": round(one * 1e3, 3)}
+  out = {"workload": "config 1: bfp8 GEMV x[1,576] @ W[576,1536], fp32 out", "bytes": nbytes, "copies": copies}
+  for axis, key in ((lib.AXIS_N, ""), (lib.AXIS_K, "along_k_")):
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    ws = [ops.pack(torch.randn(K, N, generator=g, device=dev) * 0.02, "bfp8", axis=axis) for _ in range(copies)]
+    x = torch.randn(1, K, generator=g, device=dev).to(torch.bfloat16).float()
+    y = torch.empty(1, N, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    def many():
+      for w in ws: ops.gemv(x, w, out=y)
+    ms = timed_graph(many, reps, stream) / copies
+    one = timed_graph(lambda: [ops.gemv(x, ws[0], out=y) for _ in range(copies)], reps, stream) / copies
+    del ws
+    torch.cuda.empty_cache()
+    out |= {key + "us": round(ms * 1e3, 3), key + "gbs": round(nbytes / ms / 1e6, 1),
+            key + "us_cache_resident": round(one * 1e3, 3)}
+  return out
 
 
 def config2_rate(dev, steps=50, warmup=5, place=143):

@@ -48,6 +48,7 @@ SIGNATURES = {
   "fh_bfp_pack": ([P, I, L, L, L, I, I, P, P, P], I),
   "fh_bfp_dequant": ([P, P, L, L, I, I, P, L, P], I),
   "fh_gemv_bfp": ([P, I, L, I, L, L, P, P, I, ctypes.POINTER(Epilogue), P, I, L, P], I),
+  "fh_gemv_bfp_k": ([P, I, L, I, L, L, P, P, I, ctypes.POINTER(Epilogue), P, I, L, P], I),
   "fh_gemm_bfp": ([P, I, L, L, L, L, P, P, I, ctypes.POINTER(Epilogue), P, I, L, P], I),
   "fh_matmul": ([P, I, L, L, P, I, L, L, L, L, L, L, ctypes.POINTER(Program), P, I, L, L, P], I),
   "fh_embed_rows": ([P, I, L, L, P, I, P, P, P], I),

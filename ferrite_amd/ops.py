@@ -164,7 +164,9 @@ def _layout(t):
 
 
 def _matmul(entry, x, bw, ep, out, out_dtype):
-  if bw.axis != lib.AXIS_N: raise NotImplementedError(f"{entry}: weights packed along N")
+  if bw.axis != lib.AXIS_N:
+    if entry != "fh_gemv_bfp": raise NotImplementedError(f"{entry}: weights packed along N (along K: the GEMV)")
+    entry = "fh_gemv_bfp_k"
   if isinstance(x, Tiles16):
     if x.cols != bw.K: raise ValueError(f"{entry}: x tiles of {x.cols} columns for W {bw.K}x{bw.N}")
   elif x.dim() != 2 or x.shape[1] != bw.K or x.stride(1) != 1: raise ValueError(f"{entry}: x {tuple(x.shape)} for W {bw.K}x{bw.N}")
@@ -182,7 +184,8 @@ def _matmul(entry, x, bw, ep, out, out_dtype):
 
 
 def gemv(x, bw, ep=None, out=None, out_dtype=torch.float32):
-  """y = x @ W with the epilogue ep (fh_gemv_bfp): a few rows, fp32 x, exact products. W packed along N."""
+  """y = x @ W with the epilogue ep: a few rows, fp32 x, exact products. W packed along N (fh_gemv_bfp), or along K
+  (fh_gemv_bfp_k: the store, residual and program epilogues)."""
   return _matmul("fh_gemv_bfp", x, bw, ep, out, out_dtype)
 
 

@@ -168,6 +168,16 @@ typedef struct fh_epilogue {
 int fh_gemv_bfp(const void* x, int x_dtype, int64_t ldx, int batch, int64_t K, int64_t N, const void* w_mant,
                 const uint8_t* w_exps, int fmt, const fh_epilogue* ep, void* y, int y_dtype, int64_t ldy, void* stream);
 
+/* fh_gemv_bfp for a weight packed along K (FH_AXIS_K: each run of 16 consecutive rows of a column shares an
+ * exponent, gpt2.bfp(W.T).T, models/gpt2.py:21-32 applied to W's transpose): y = epilogue(prologue(x) @ W), K a
+ * multiple of 16, any N >= 1. Epilogues FH_EP_STORE (argmax_parts with N a multiple of 16), FH_EP_RESIDUAL and
+ * FH_EP_PROGRAM, the RMSNorm prologue as fh_gemv_bfp's; the pairs (FH_EP_SILU_GATE, FH_EP_ROPE_KV) are
+ * FH_EUNSUP. Products exact (each run's sum of x q in fp32, times the run's power of 2), waves' sums in a fixed order.
+ * Replaces fused_kernel's matmul by a block-float B whose blocks run down its columns (ferrite/compiler.py:699-1111
+ * with the tile's face rows along K: the benchmark's config 1 as stated, 16-element blocks along K). */
+int fh_gemv_bfp_k(const void* x, int x_dtype, int64_t ldx, int batch, int64_t K, int64_t N, const void* w_mant,
+                  const uint8_t* w_exps, int fmt, const fh_epilogue* ep, void* y, int y_dtype, int64_t ldy, void* stream);
+
 /* ---- prefill GEMM: the same y = epilogue(prologue(x) @ W) for M rows, on the matrix cores ----------------------
  * x: [M][K] fp32 or bf16 (row stride ldx, a multiple of 8); K a multiple of 32. As ferrite's chip does (its unpacker
  * hands the matrix unit bf16; ferrite/tensor.py:443-485), the products are bf16 x bf16 with fp32 sums: x (times the

@@ -3,7 +3,9 @@ in Llama-3.1-8B's shapes against numpy), through the C-ABI:
 - config 3: two Llama-3.1-8B-shape blocks (4096 wide, 32 query heads sharing 8 key heads of 128, MLP 14336, vocab
   128256, Llama 3's RoPE) at precision "experts" (attention and output layer bfp8, MLP bfp4), a bf16 KV cache at
   context 2048: a batch-1 step at place 2047 (the GEMV path) and a batch-16 step of 16 sequences at places up to 2047
-  (the skinny matrix-core path);
+  (the skinny matrix-core path); a 64-token prompt then 32 greedy steps of batch 1, the same tokens as numpy's
+  (models/llama.py:787-796); and the reference's own case at "tt" precision with a bfp8 cache (a 64-token prompt,
+  two decode steps);
 - config 4: a 2048-token prefill of two such blocks, all bfp8 (the tiled MFMA GEMM and the causal prefill attention),
   its keys and values and last logits, then a decode step from the cache it filled;
 - config 5: a Mixtral-shape mixture of experts (4096 wide, 8 experts of MLP 14336 in bfp4, top 2) over 32 tokens.
@@ -179,3 +181,64 @@ def test_config5_moe_mixtral_width(cuda):
   got = y.cpu().numpy()
   north_star(got, want, "config 5 MoE, 32 tokens")
   for t in range(T): north_star(got[t], want[t], f"config 5 token {t}")
+
+
+def test_config3_prompt_then_32_greedy_tokens(m8b):
+  # models/llama.py's main at config 3's width (its check of every step against numpy, models/llama.py:787-796): two
+  # Llama-3.1-8B-shape blocks at precision "experts", a bf16 cache, a 64-token seeded prompt (one step of 64 rows, the
+  # exact-product GEMV), then 32 greedy steps of batch 1 (the benchmark's step, replayed as a graph), each fed its own
+  # pick; numpy's model as written (float64, its cache unrounded) does the same. The 32 tokens must be the same; each
+  # step's logits within the north star's bar, and each step's top-1 / top-2 gap printed beside its error
+  from ferrite_amd import llama as G
+  c, ctx, P, steps = m8b.c, 128, 64, 32
+  c.precision = OL.precision(c, "experts", "bf16")
+  w = m8b.oracle("experts")
+  prompt = [int(i) for i in np.random.default_rng(38).integers(0, c.vocab, P)]
+  np_kv = OL.kv_cache(c, ctx)
+  want, want_logits, new, places = [], [], prompt, list(range(P))
+  for i in range(steps):
+    logits = OL.forward(new, places, w, c, np_kv)[0]
+    want_logits.append(logits)
+    want.append(int(np.argmax(logits)))
+    new, places = [want[-1]], [P + i]
+  first = G.Decoder(m8b.gc, m8b.draw, mode="experts", kv="bf16", batch=P, context=ctx, mfma_from=None)
+  logits, picks = first.step(prompt, list(range(P)), replay=False)
+  got_logits, got = [logits[-1].cpu().numpy().astype(np.float64)], [int(picks[-1])]
+  one = G.Decoder(m8b.gc, None, mode="experts", kv="bf16", batch=1, context=ctx, share=first)
+  for l in range(c.layers): one.cache[l].copy_(first.cache[l])
+  del first
+  one.step([got[-1]], [P])
+  for i in range(1, steps):
+    got_logits.append(one.logits[0].cpu().numpy().astype(np.float64))
+    got.append(int(one.picks[0]))
+    one.advance()
+    one.step()
+  for i, (a, b) in enumerate(zip(want_logits, got_logits)):
+    top = np.sort(a)[-2:]
+    err = float(np.abs(a - b).max())
+    print(f"step {i}: token {want[i]} (GPU {got[i]}), top-1 - top-2 gap {top[1] - top[0]:.3e}, logits' largest error "
+          f"{err:.3e} of {np.abs(a).max():.3e}", flush=True)
+    north_star(b, a, f"config 3 greedy step {i} logits")
+  assert got == want, (got, want)
+
+
+def test_config3_tt_precision_bfp8_cache(m8b):
+  # the reference's own 8B-shape case (test_llama_8b_shapes, test/test_sim.py:1926-1949): TT's performance precision
+  # ("tt": gate_up bfp4, the rest bfp8) with its bfp8 KV cache, a 64-token prompt (here the prefill on the matrix
+  # cores) and two decode steps (tokens 5 at place 64 and 9 at 65, the GEMV path); each time the pick the same as
+  # numpy's and the logits within 2% of numpy's span (its bar, np.ptp)
+  from ferrite_amd import llama as G
+  c, ctx = m8b.c, 96
+  c.precision = OL.precision(c, "tt", "bfp8")
+  w = m8b.oracle("tt")
+  dec = G.Decoder(m8b.gc, m8b.draw, mode="tt", kv="bfp8", batch=1, context=ctx)
+  np_kv = OL.kv_cache(c, ctx)
+  prompt = [int(i) for i in np.random.default_rng(8).integers(0, c.vocab, 64)]
+  for new, places in ((prompt, list(range(64))), ([5], [64]), ([9], [65])):
+    if len(new) > 1: got = dec.prefill(new)[0][0].cpu().numpy().astype(np.float64)
+    else: got = dec.step(new, places, replay=False)[0][0].cpu().numpy().astype(np.float64)
+    want = OL.forward(new, places, w, c, np_kv)[0]
+    err, span = float(np.abs(got - want).max()), float(np.ptp(want))
+    print(f"tt, bfp8 cache, places {places[0]}..{places[-1]}: logits' largest error {err:.3e}, numpy's span {span:.3e}",
+          flush=True)
+    assert int(np.argmax(got)) == int(np.argmax(want)) and err < 0.02 * span, (places[0], err, span)

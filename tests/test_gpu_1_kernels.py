@@ -126,6 +126,74 @@ def test_gemv_shapes_and_batches(cuda, fmt):
       check_close(y, O.gemv(x, wv), 2e-6 * (np.abs(x) @ np.abs(wv)) + 1e-30, (K, N, batch))
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+def test_gemv_config1_blocks_along_k(cuda, fmt):
+  # benchmark config 1 as its text states it: W[576,1536] packed with its 16-element blocks along K (each run 16
+  # consecutive rows of a column, gpt2.bfp(W.T).T), y = x @ W in fp32 by fh_gemv_bfp_k; against the oracle's
+  # bfp(W, axis=0) in float64 within fp32 summation's error (2e-6 of sum |x w|) and the north star's bar; the
+  # dequantised weight bit for bit the oracle's; batches up to 11 rows (past 8: two launches), an N off 64 and 16
+  L = lib()
+  rng = np.random.default_rng(9)
+  x = O.bf16(rng.normal(0, 1, (1, 576)))
+  w = rng.normal(0, 0.02, (576, 1536)).astype(np.float32)
+  bw = ops().pack(to_gpu(w), fmt, axis=L.AXIS_K)
+  wv = O.bfp(w, fmt, axis=0)
+  assert not np.array_equal(wv, O.bfp(w, fmt))  # (a different block float from ferrite's own, N-blocked one)
+  got = ops().dequant(bw).view(torch.int16).cpu().numpy().view(np.uint16)
+  assert np.array_equal(O.bf16_floats(got), wv.astype(np.float32)), fmt
+  y = ops().gemv(to_gpu(x), bw).cpu().numpy()
+  check_close(y, O.gemv(x, wv), 2e-6 * (np.abs(x) @ np.abs(wv)) + 1e-30, ("config 1 along K", fmt))
+  for K, N in ((16, 5), (64, 100), (1536, 576), (4096, 256)):
+    w = wide(rng, (K, N)) * 0.02
+    bw = ops().pack(to_gpu(w), fmt, axis=L.AXIS_K)
+    wv = O.bfp(w, fmt, axis=0)
+    for batch in (1, 3, 8, 11):
+      x = rng.normal(0, 1, (batch, K)).astype(np.float32)
+      y = ops().gemv(to_gpu(x), bw).cpu().numpy()
+      check_close(y, O.gemv(x, wv), 2e-6 * (np.abs(x) @ np.abs(wv)) + 1e-30, ("along K", K, N, batch))
+
+
+def test_gemv_along_k_exact_and_epilogues(cuda):
+  # integers times a power of 2 per run down each column: every product and partial sum exact, so y is bit for bit;
+  # x @ I picks out x exactly; then the residual epilogue (with its sums of squares by 16 columns and a bf16 copy), the
+  # RMSNorm prologue and a program epilogue, against numpy on the same values
+  L = lib()
+  rng = np.random.default_rng(10)
+  K, N = 256, 64
+  w = (rng.integers(-7, 8, (K, N)) * 2.0 ** rng.integers(-3, 3, (1, N))).astype(np.float32)
+  x = rng.integers(-4, 5, (3, K)).astype(np.float32)
+  for fmt in ("bfp8", "bfp4"):
+    wv = O.bfp(w, fmt, axis=0)
+    y = ops().gemv(to_gpu(x), ops().pack(to_gpu(w), fmt, axis=L.AXIS_K)).cpu().numpy()
+    assert np.array_equal(y, (x.astype(np.float64) @ wv).astype(np.float32)), fmt
+  eye = np.eye(64, dtype=np.float32)
+  xe = O.bf16(rng.normal(0, 1, (2, 64)))
+  assert np.array_equal(ops().gemv(to_gpu(xe), ops().pack(to_gpu(eye), axis=L.AXIS_K)).cpu().numpy(), xe)
+  K, N = 576, 1536
+  w = rng.normal(0, 0.02, (K, N)).astype(np.float32)
+  bw = ops().pack(to_gpu(w), "bfp8", axis=L.AXIS_K)
+  wv = O.bfp(w, "bfp8", axis=0)
+  x = rng.normal(0, 1, (2, K)).astype(np.float32)
+  res = rng.normal(0, 1, (2, N)).astype(np.float32)
+  y, ssq = to_gpu(res.copy()), torch.zeros(2, N // 16, device="cuda")
+  copy = torch.zeros(2, N, dtype=torch.bfloat16, device="cuda")
+  ops().gemv(to_gpu(x), bw, ops().epilogue(L.EP_RESIDUAL, residual=y, ssq_out=ssq, copy_bf16=copy), out=y)
+  want = res + O.gemv(x, wv)
+  bound = 2e-6 * (np.abs(x) @ np.abs(wv) + np.abs(res)) + 1e-30
+  check_close(y.cpu().numpy(), want, bound, "residual along K")
+  g = y.cpu().numpy().astype(np.float64)
+  assert np.allclose(ssq.cpu().numpy(), (g * g).reshape(2, -1, 16).sum(-1), rtol=1e-5)
+  assert np.array_equal(copy.float().cpu().numpy(), O.bf16(y.cpu().numpy()))
+  # the RMSNorm prologue: x * rsqrt(mean(x^2) + eps) * norm_w, from x's sums of squares by 16
+  nw = rng.normal(1, 0.1, K).astype(np.float32)
+  xs = to_gpu(x)
+  ssq_in = to_gpu((x.astype(np.float64) ** 2).reshape(2, -1, 16).sum(-1).astype(np.float32))
+  y = ops().gemv(xs, bw, ops().epilogue(L.EP_STORE, norm_w=to_gpu(nw), ssq_in=ssq_in, eps=1e-5)).cpu().numpy()
+  c = OL.model(dim=K, eps=1e-5)
+  xn = OL.rms(x.astype(np.float64), nw.astype(np.float64), c)
+  check_close(y, xn @ wv, 4e-6 * (np.abs(xn) @ np.abs(wv)) + 1e-30, "RMSNorm prologue along K")
+
+
 def test_gemv_exact_integers(cuda):
   # small integers times a power of 2 per run: every product and partial sum exact in fp32, so y is bit for bit
   # (test_matmul_exact's idea, test/test_sim.py:310-323); and x @ I picks out x's columns exactly

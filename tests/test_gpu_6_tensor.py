@@ -158,15 +158,16 @@ def test_matmul_and_its_chain(rt, rows):
   assert rt.launches - before == 2, rt.launches - before  # the matmul with its chain, then the softmax
   e = np.exp(want - want.max(-1, keepdims=True))
   close(s, e / e.sum(-1, keepdims=True), 1e-4, ("softmax", rows))
-  # Runtime.profile (ferrite/runtime.py:416-428): each launch's time and the bytes it read, by name. The matmul read
-  # the packed weight (K N 17/16 bytes), x's bf16 rows and the bias row once; the softmax its fp32 rows
+  # Runtime.profile (ferrite/runtime.py:416-428): each launch's time and the bytes it read, by name. The first matmul
+  # read the packed weight (K N 17/16 bytes), x's bf16 rows and the bias row once; the second, under a softmax, the
+  # weight and x only (its chain goes into the softmax's program, which reads the fp32 rows and the bias)
   since = rt.launches
   (X @ W + Bias).relu().float().realize()
   (X.matmul(W, "fp32") + Bias).relu().softmax().realize()
   got = {name: (n, us, b) for name, n, us, b in rt.profile(since)}
   assert got["matmul"][0] == 2 and got["matmul"][1] > 0 and got["softmax"][0] == 1
-  assert got["matmul"][2] == 2 * (K * N * 17 // 16 + rows * K * 2 + N * 2), got["matmul"]
-  assert got["softmax"][2] == rows * N * 4, got["softmax"]
+  assert got["matmul"][2] == 2 * (K * N * 17 // 16 + rows * K * 2) + N * 2, got["matmul"]
+  assert got["softmax"][2] == rows * N * 4 + N * 2, got["softmax"]
 
 
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
