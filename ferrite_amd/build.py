@@ -10,6 +10,9 @@ ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
          # packed fp32 ops are left to nobody: hipcc would make them from plain float code
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # a kernel's leading scalar arguments arrive in SGPRs with its waves (gfx950 kernel-argument preloading), so
+         # the first loads of the hot kernels do not wait on the argument buffer
+         "-mllvm", "-amdgpu-kernarg-preload-count=16",
          "-I", str(HERE.parent / "include")]
 
 

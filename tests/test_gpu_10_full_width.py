@@ -183,43 +183,65 @@ def test_config5_moe_mixtral_width(cuda):
   for t in range(T): north_star(got[t], want[t], f"config 5 token {t}")
 
 
-def test_config3_prompt_then_32_greedy_tokens(m8b):
-  # models/llama.py's main at config 3's width (its check of every step against numpy, models/llama.py:787-796): two
-  # Llama-3.1-8B-shape blocks at precision "experts", a bf16 cache, a 64-token seeded prompt (one step of 64 rows, the
-  # exact-product GEMV), then 32 greedy steps of batch 1 (the benchmark's step, replayed as a graph), each fed its own
-  # pick; numpy's model as written (float64, its cache unrounded) does the same. The 32 tokens must be the same; each
-  # step's logits within the north star's bar, and each step's top-1 / top-2 gap printed beside its error
+def greedy_8b(m8b, kv, forced):
+  """A 64-token seeded prompt (one step of 64 rows, the exact-product GEMV), then 31 more steps of batch 1 (the
+  benchmark's step, replayed as a graph) at precision "experts": numpy's model as written (float64, its cache
+  unrounded) and the GPU each fed its own pick, or (forced) both fed numpy's pick, as models/llama.py's main does
+  (787-796: "so that one near tie does not send the two down different paths"). Returns numpy's and the GPU's picks
+  and logits, step by step."""
   from ferrite_amd import llama as G
   c, ctx, P, steps = m8b.c, 128, 64, 32
-  c.precision = OL.precision(c, "experts", "bf16")
+  c.precision = OL.precision(c, "experts", kv)
   w = m8b.oracle("experts")
   prompt = [int(i) for i in np.random.default_rng(38).integers(0, c.vocab, P)]
   np_kv = OL.kv_cache(c, ctx)
-  want, want_logits, new, places = [], [], prompt, list(range(P))
+  first = G.Decoder(m8b.gc, m8b.draw, mode="experts", kv=kv, batch=P, context=ctx, mfma_from=None)
+  one = G.Decoder(m8b.gc, None, mode="experts", kv=kv, batch=1, context=ctx, share=first)
+  want, got, wl, gl = [], [], [], []
+  new, places = prompt, list(range(P))
   for i in range(steps):
-    logits = OL.forward(new, places, w, c, np_kv)[0]
-    want_logits.append(logits)
-    want.append(int(np.argmax(logits)))
-    new, places = [want[-1]], [P + i]
-  first = G.Decoder(m8b.gc, m8b.draw, mode="experts", kv="bf16", batch=P, context=ctx, mfma_from=None)
-  logits, picks = first.step(prompt, list(range(P)), replay=False)
-  got_logits, got = [logits[-1].cpu().numpy().astype(np.float64)], [int(picks[-1])]
-  one = G.Decoder(m8b.gc, None, mode="experts", kv="bf16", batch=1, context=ctx, share=first)
-  for l in range(c.layers): one.cache[l].copy_(first.cache[l])
-  del first
-  one.step([got[-1]], [P])
-  for i in range(1, steps):
-    got_logits.append(one.logits[0].cpu().numpy().astype(np.float64))
-    got.append(int(one.picks[0]))
-    one.advance()
-    one.step()
-  for i, (a, b) in enumerate(zip(want_logits, got_logits)):
+    a = OL.forward(new, places, w, c, np_kv)[0]
+    if i == 0:
+      logits, picks = first.step(prompt, places, replay=False)
+      b = logits[-1].cpu().numpy().astype(np.float64)
+      for l in range(c.layers): one.cache[l].copy_(first.cache[l])
+    else:
+      logits, picks = one.step([nxt], [P + i - 1])
+      b = logits[0].cpu().numpy().astype(np.float64)
+    want.append(int(np.argmax(a)))
+    got.append(int(picks[-1]))
+    wl.append(a)
+    gl.append(b)
+    nxt = want[-1] if forced else got[-1]
+    new, places = [want[-1]] if forced else [got[-1]], [P + i]
+  return want, got, wl, gl
+
+
+def test_config3_prompt_then_32_greedy_tokens(m8b):
+  # models/llama.py's main at config 3's width (its check of every step against numpy, models/llama.py:787-796), two
+  # Llama-3.1-8B-shape blocks at precision "experts", 32 steps (the prompt's and 31 greedy ones). An fp32 cache: the
+  # GPU's logits within fp32 summation of numpy's (1e-4 of the largest), and each fed its own pick, the 32 tokens the
+  # same. The benchmark's bf16 cache rounds each key and value (2^-9 relative), which moves the logits by up to ~3e-3
+  # of their largest: both fed numpy's pick, as the reference's main feeds them, each step within the north star's
+  # bar, and the picks the same at every step whose top-1 / top-2 gap is more than twice that step's largest error
+  # (a nearer tie goes either way; its count printed)
+  want, got, wl, gl = greedy_8b(m8b, "fp32", forced=False)
+  for i, (a, b) in enumerate(zip(wl, gl)):
+    top = np.sort(a)[-2:]
+    rel = float(np.abs(a - b).max() / np.abs(a).max())
+    print(f"fp32 cache, step {i}: token {want[i]} (GPU {got[i]}), gap {top[1] - top[0]:.3e}, error {rel:.2e} of the largest", flush=True)
+    assert rel <= 1e-4, (i, rel)
+  assert got == want, (got, want)
+  want, got, wl, gl = greedy_8b(m8b, "bf16", forced=True)
+  ties = 0
+  for i, (a, b) in enumerate(zip(wl, gl)):
     top = np.sort(a)[-2:]
     err = float(np.abs(a - b).max())
-    print(f"step {i}: token {want[i]} (GPU {got[i]}), top-1 - top-2 gap {top[1] - top[0]:.3e}, logits' largest error "
-          f"{err:.3e} of {np.abs(a).max():.3e}", flush=True)
-    north_star(b, a, f"config 3 greedy step {i} logits")
-  assert got == want, (got, want)
+    print(f"bf16 cache, step {i}: token {want[i]} (GPU {got[i]}), gap {top[1] - top[0]:.3e}, error {err:.3e}", flush=True)
+    north_star(b, a, f"config 3 bf16 cache, step {i} logits")
+    if top[1] - top[0] > 2 * err: assert got[i] == want[i], (i, got[i], want[i])
+    else: ties += 1
+  print(f"bf16 cache: the same pick at {sum(g == w for g, w in zip(got, want))} of 32 steps, {ties} near ties")
 
 
 def test_config3_tt_precision_bfp8_cache(m8b):
