@@ -88,6 +88,24 @@ __device__ inline void magnitudes8(const uint32_t& m, float (&f)[8]) {
   }
 }
 
+// bfp4's 16 magnitudes offset by 8, through the chip's fp8 converter: a nibble's two's-complement q XOR 8 is q + 8 in
+// 0..15, and an fp8 (OCP E4M3) byte of 0..15 is that integer times 2^-9 exactly (subnormal below 8, exponent field 1
+// above), so f[j] = (q_j + 8) 2^-9. Per 8 values: a shift, two three-input bit operations (mask, then XOR 8) and four
+// conversions of two values each (v_cvt_pk_f32_fp8), against a convert a value for magnitudes(). The caller takes
+// the 8 2^-9 back out (once for all 16 columns: the sum of its scales times 2^-6).
+typedef float fh_float2 __attribute__((ext_vector_type(2)));
+__device__ inline void magnitudes_off8(const uint2& m, float (&f)[16]) {
+  const uint32_t w[2] = {m.x, m.y};
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const uint32_t lo = (w[d] & 0x0F0F0F0Fu) ^ 0x08080808u, hi = ((w[d] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+    const fh_float2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false), b = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+    const fh_float2 c = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false), e = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);
+    f[8 * d + 0] = a.x; f[8 * d + 2] = a.y; f[8 * d + 4] = b.x; f[8 * d + 6] = b.y;  // (low nibbles: even columns)
+    f[8 * d + 1] = c.x; f[8 * d + 3] = c.y; f[8 * d + 5] = e.x; f[8 * d + 7] = e.y;
+  }
+}
+
 // N values of a run of a block float as bf16, two a word (value 2i low, 2i + 1 high), exactly: f holds q (bfp8) or
 // 16 q (bfp4, so both scale by 2^(top - 133)). q times a normal power of 2 is exact in fp32 (at most 7 significant
 // bits) and its upper half is its bf16; a scale below fp32's normals (top < 7) takes bfp_value_bf16's integer path.

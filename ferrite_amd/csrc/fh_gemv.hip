@@ -91,6 +91,12 @@ __global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(const uint8_t* __
       for (int b = 0; b < B; ++b) xv[u][b] = xf[b * ldx + k];
     }
   };
+  // bfp4: each value as (q + 8) 2^-9 (magnitudes_off8), its row's scale x 2^(e - 120) so that the products are
+  // x (q + 8) 2^(e - 129); the 8 comes back out at the end, the lane's sum of its rows' scales times 2^-6 off each of
+  // the run's 16 sums (exact products either way, the sums' rounding of the same order)
+  float off[B * P];
+#pragma unroll
+  for (int i = 0; i < B * P; ++i) off[i] = 0.f;
   auto compute = [&](int k0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -100,10 +106,15 @@ __global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(const uint8_t* __
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         float f[16];
-        magnitudes(m[u][p], f);
+        if constexpr (FOUR) magnitudes_off8(m[u][p], f);
+        else magnitudes(m[u][p], f);
         float xs[B];
 #pragma unroll
-        for (int b = 0; b < B; ++b) xs[b] = ok ? ldexpf(xv[u][b] * gw, e[u][p] - 133) : 0.f;
+        for (int b = 0; b < B; ++b) xs[b] = ok ? ldexpf(xv[u][b] * gw, e[u][p] - (FOUR ? 120 : 133)) : 0.f;
+        if constexpr (FOUR) {
+#pragma unroll
+          for (int b = 0; b < B; ++b) off[b * P + p] += xs[b];
+        }
 #pragma unroll
         for (int j = 0; j < 16; ++j)
 #pragma unroll
@@ -126,6 +137,12 @@ __global__ __launch_bounds__(gemv_threads(B)) void gemv_kernel(const uint8_t* __
     compute(k0);
   }
 
+  if constexpr (FOUR) {  // the offset's products out: 8 2^-9 times the scales' sum
+#pragma unroll
+    for (int i = 0; i < B * P; ++i)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[i * 16 + j] = fmaf(off[i], -0.015625f, acc[i * 16 + j]);
+  }
   // each run of 16 across the wave: lane holds the sum of value reduce16_index(lane) of each group in sums[g]
   float sums[G];
 #pragma unroll
