@@ -2,7 +2,7 @@
 attention and the output layer in bfp8, every MLP matrix in bfp4, a bf16 KV cache at context 2048, batch 1).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c3-bfp8|c2] [--batch B] [--no-cpu] [--no-prefill]
-                [--only bs16|prefill|moe|floor|peaks]
+                [--only bs16|prefill|moe|floor|peaks|c1|c2]
 
 Prints ONE JSON line: tokens/s of the whole decode step (every kernel of it replayed as one HIP graph, inputs resident
 in HBM), the dominant GEMV's achieved HBM bandwidth against the 8 TB/s peak (timed live with HIP events on its own
@@ -12,8 +12,8 @@ its own field, with the same step with every matrix bfp8 (`decode_bfp8`), batche
 `configs` holds config 1's GEMV and config 2's SmolLM step on the GPU, and the numpy CPU baselines of configs 1, 2, 4
 and 5 (bounded samples, each saying how it was scaled). Synthetic data: random-init weights, drawn on the GPU and
 packed there. --only runs one part by itself and prints its fields as the JSON line (what a profiler run of one part
-uses): the batch-16 step, config 4's prefill, config 5's MoE layer, the read floor (read_floor), or the matrix
-cores' and LDS's own rates (core_peaks)."""
+uses): the batch-16 step, config 4's prefill, config 5's MoE layer, the read floor (read_floor), the matrix cores'
+and LDS's own rates (core_peaks), config 1's GEMVs or config 2's SmolLM step."""
 import argparse, json, os, statistics, sys, time
 import numpy as np
 import torch
@@ -515,7 +515,7 @@ def main():
   ap.add_argument("--batch", type=int, default=1)
   ap.add_argument("--no-cpu", action="store_true")
   ap.add_argument("--no-prefill", action="store_true", help="skip config 4's prefill measurement")
-  ap.add_argument("--only", choices=("bs16", "prefill", "moe", "floor", "peaks"), help="run one part alone (see above)")
+  ap.add_argument("--only", choices=("bs16", "prefill", "moe", "floor", "peaks", "c1", "c2"), help="run one part alone (see above)")
   ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                   help="first run a plain copy kernel (torch.neg) over MIB MiB: the known-size kernel that calibrates "
                        "rocprofv3's FETCH_SIZE/WRITE_SIZE counters in the same run")
@@ -542,6 +542,8 @@ def main():
     elif args.only == "prefill": r = prefill_rate()
     elif args.only == "moe": r = {"moe": moe_rate(), "moe_prompt": moe_rate(2048, reps=5)}
     elif args.only == "peaks": r = core_peaks(dev)
+    elif args.only == "c1": r = config1_rate(dev)
+    elif args.only == "c2": r = config2_rate(dev)
     else: r = read_floor(dev)
     print(json.dumps({"only": args.only, **r}), flush=True)
     return
