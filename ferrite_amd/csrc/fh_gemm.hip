@@ -51,6 +51,84 @@ __device__ inline int64_t tile_run(const MatArgs& a, int tn, int lr) {
   return lr < 4 ? nb0 : nb0 + a.pair_half;
 }
 
+// The tile's epilogue: every output of the fp32 tile Cs [BM][GM_LDC] (staged in LDS: each output sees its row's 1/rms
+// and its pair partner, whichever wave computed it) through a's epilogue, NT threads
+template <int BM, int NT>
+__device__ inline void gemm_epilogue(const MatArgs& a, const SkinnyMoe& g, const float* Cs, const float* rs_s, int tn,
+                                     int64_t m0, int64_t M, int64_t ybase, int t) {
+  const int kind = a.kind;
+  if (a.P == 1 && kind == FH_EP_PROGRAM) {  // (a loop of its own: the program's decoding, hoisted out of the loop,
+                                            // runs only here)
+    const int c = t & 127;
+    const int64_t run = tile_run(a, tn, c >> 4);
+    const int64_t col = run * 16 + (c & 15);
+    for (int r = t >> 7; r < BM; r += NT / 128) {
+      const int64_t m = m0 + r;
+      if (m < M && run >= 0)
+        store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + col, prog_eval(a.prog, Cs[r * GM_LDC + c] * rs_s[r], 0, m, col));
+    }
+  } else if (a.P == 1) {  // FH_EP_STORE, FH_EP_RESIDUAL: a thread a column, 2 rows a pass; a run is 16 lanes
+    const int c = t & 127, j = c & 15;
+    const int64_t run = tile_run(a, tn, c >> 4);
+    const int64_t col = run * 16 + j;
+    for (int r = t >> 7; r < BM; r += NT / 128) {
+      const int64_t m = m0 + r;
+      const bool ok = m < M && run >= 0;
+      const int64_t at = (ybase + m) * a.ldy + col;
+      float v = Cs[r * GM_LDC + c] * rs_s[r];
+      if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
+      if (ok) store_out(a.y, a.y_bf16, at, v);
+      if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) put_copy(a, m, col, v);
+      if (kind == FH_EP_RESIDUAL && a.ssq_out) {
+        float s = v * v;
+        s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
+        if (ok && j == 0) a.ssq_out[m * (a.N / 16) + run] = s;
+      }
+      if (kind == FH_EP_STORE && a.argmax_parts) {
+        float bv = v;
+        int bc = (int)col;
+#pragma unroll
+        for (int s = 8; s >= 1; s >>= 1) {
+          const float ov = __shfl_xor(bv, s, 64);
+          const int oc = __shfl_xor(bc, s, 64);
+          if (ov > bv || (ov == bv && oc < bc)) { bv = ov; bc = oc; }
+        }
+        if (ok && j == 0) a.argmax_parts[m * (a.N / 16) + run] = make_int2(__float_as_int(bv), bc);
+      }
+    }
+  } else {  // the pairs: a thread a (first-half) column, 4 rows a pass
+    const int c = t & 63, p = c >> 4, j = c & 15;
+    const int64_t run = tile_run(a, tn, p);
+    const int64_t c0 = run * 16 + j;
+    for (int r = t >> 6; r < BM; r += NT / 64) {
+      const int64_t m = m0 + r;
+      if (m >= M || run < 0) continue;
+      float x0 = Cs[r * GM_LDC + c] * rs_s[r], x1 = Cs[r * GM_LDC + c + 64] * rs_s[r];
+      if (kind == FH_EP_SILU_GATE) {
+        const float sc = g.scale_rows ? g.row_w[ybase + m] : 1.f;
+        store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + c0, silu(x0) * x1 * sc);
+      } else {  // FH_EP_ROPE_KV
+        const int hd = a.head_dim;
+        const int h = (int)c0 / hd, d = (int)c0 % hd, d1 = d + hd / 2;  // (c0 < N < 2^31)
+        if (h < a.heads + a.kv_heads) {  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
+          const int64_t place = rope_place(a, a.places[m]);
+          const float* cs = a.cos_tab + place * hd;
+          const float* sn = a.sin_tab + place * hd;
+          const float t0 = x0 * cs[d] - x1 * sn[d], t1 = x1 * cs[d1] + x0 * sn[d1];
+          x0 = t0; x1 = t1;
+        }
+        if (h < a.heads) {
+          float* q = (float*)a.y + m * a.ldy + (int64_t)h * hd;
+          q[d] = x0; q[d1] = x1;
+        } else {
+          const int ch = h - a.heads;
+          cache_put(a, ch, a.cache_rows[m], d, d1, j, x0, x1);
+        }
+      }
+    }
+  }
+}
+
 template <bool FOUR, bool XBF16, bool NORM, int TM>  // TM: 128-row halves of the tile (1, or 2 with 8 waves)
 __global__ __launch_bounds__(GM_THREADS * TM, 3 - TM) void gemm_kernel(MatArgs a, int tiles_m, int tiles_n, SkinnyMoe g) {
   constexpr int BM = GM_BM * TM, NT = GM_THREADS * TM;
@@ -259,77 +337,191 @@ __global__ __launch_bounds__(GM_THREADS * TM, 3 - TM) void gemm_kernel(MatArgs a
         Cs[(wr + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * GM_LDC + wc + 32 * j + (lane & 31)] = acc[i][j][r];
   __syncthreads();
 
-  const int kind = a.kind;
-  if (a.P == 1 && kind == FH_EP_PROGRAM) {  // (a loop of its own: the program's decoding, hoisted out of the loop,
-                                            // runs only here)
-    const int c = t & 127;
-    const int64_t run = tile_run(a, tn, c >> 4);
-    const int64_t col = run * 16 + (c & 15);
-    for (int r = t >> 7; r < BM; r += NT / 128) {
-      const int64_t m = m0 + r;
-      if (m < M && run >= 0)
-        store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + col, prog_eval(a.prog, Cs[r * GM_LDC + c] * rs_s[r], 0, m, col));
-    }
-  } else if (a.P == 1) {  // FH_EP_STORE, FH_EP_RESIDUAL: a thread a column, 2 rows a pass; a run is 16 lanes
-    const int c = t & 127, j = c & 15;
-    const int64_t run = tile_run(a, tn, c >> 4);
-    const int64_t col = run * 16 + j;
-    for (int r = t >> 7; r < BM; r += NT / 128) {
-      const int64_t m = m0 + r;
-      const bool ok = m < M && run >= 0;
-      const int64_t at = (ybase + m) * a.ldy + col;
-      float v = Cs[r * GM_LDC + c] * rs_s[r];
-      if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
-      if (ok) store_out(a.y, a.y_bf16, at, v);
-      if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) put_copy(a, m, col, v);
-      if (kind == FH_EP_RESIDUAL && a.ssq_out) {
-        float s = v * v;
-        s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
-        if (ok && j == 0) a.ssq_out[m * (a.N / 16) + run] = s;
-      }
-      if (kind == FH_EP_STORE && a.argmax_parts) {
-        float bv = v;
-        int bc = (int)col;
+  gemm_epilogue<BM, NT>(a, g, Cs, rs_s, tn, m0, M, ybase, t);
+}
+
+// The same GEMM in the two-group ("ping-pong") form, for bf16 rows with no RMSNorm prologue (a prompt's matmuls: their
+// x rows come normalised, as bf16, from fh_rms_rows, attention or SwiGLU): a workgroup of 8 waves takes a 256 x 128
+// tile, each wave a 64 x 64 quarter of a 128-row half as gemm_kernel's waves do; waves 0-3 (one a SIMD) load and
+// convert the weight, waves 4-7 (the other one a SIMD) load and copy x's rows. A K step is two phases between
+// workgroup barriers: in the first, waves 0-3 run their products on the step's LDS stage while waves 4-7 write the
+// next step's x into the other stage; in the second, waves 4-7 run their products while waves 0-3 write the next
+// step's weight. So on each SIMD one wave keeps the matrix core busy while the other does the loads, the conversion
+// and the LDS writes, and the products' wave has the higher issue priority (s_setprio). Global loads run two steps
+// ahead, in two register sets. The results are gemm_kernel's bit for bit (the same products in the same order).
+// Measured at 2048 rows of the 8B shapes against gemm_kernel in the same run: o 739 -> 796, gate_up 803 -> 842,
+// down 826 -> 922 TFLOP/s.
+template <bool FOUR>
+__global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, int tiles_m, int tiles_n, SkinnyMoe g) {
+  constexpr int BM = 2 * GM_BM, NT = 2 * GM_THREADS;
+  constexpr int STAGE = (BM + GM_BN) * GM_LD * 2;
+  constexpr int LDS = 2 * STAGE > BM * GM_LDC * 4 ? 2 * STAGE : BM * GM_LDC * 4;
+  __shared__ __attribute__((aligned(16))) char smem[LDS];
+  __shared__ float rs_s[BM];
+  float* Cs = (float*)smem;  // [256][132]: the output tile (after the K loop)
+
+  const int64_t M = a.M, ybase = 0;
+  int id = blockIdx.x;
+  if ((tiles_m * tiles_n) % 8 == 0) id = (id % 8) * (tiles_m * tiles_n / 8) + id / 8;  // (contiguous ranges an XCD)
+  const int per_group = GM_GROUP * tiles_n;
+  const int first_m = id / per_group * GM_GROUP;
+  const int gm = min(tiles_m - first_m, GM_GROUP);
+  const int tm = first_m + (id % per_group) % gm, tn = (id % per_group) / gm;
+  const int64_t m0 = (int64_t)tm * BM;
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const bool wgrp = t < GM_THREADS;  // waves 0-3: the weight; 4-7: x
+  const int K = (int)a.K;
+  const int last = (K - 1) / GM_BK * GM_BK;
+  constexpr int RB = FOUR ? 8 : 16;
+  using Half = typename std::conditional<FOUR, uint32_t, uint2>::type;  // 8 of a row's 16 magnitudes
+
+  // the weight's threads (0-255): run lr (of 8), rows 4 rq .. 4 rq + 3, columns 8 ch .. 8 ch + 7
+  const int lr = (t >> 5) & 7, rq = (t & 31) >> 1, ch = t & 1;
+  const int64_t nb = tile_run(a, tn, lr);
+  const uint8_t* mrun = a.mant + (nb < 0 ? 0 : nb) * a.K * RB + ch * (RB / 2);
+  const uint8_t* erun = a.exps + (nb < 0 ? 0 : nb) * a.K;
+  // x's threads (256-511): rows xa and xa + 128 of the tile, k half xh (32 values, 4 x 16 bytes each)
+  // (a row's two halves in neighbouring lanes: 16 lanes over 16 rows of one half write LDS without bank conflicts
+  // but load 16 lines where these load 8, and measured slower: o 796 -> 743, gate_up 842 -> 772 TFLOP/s)
+  const int tb = t & (GM_THREADS - 1), xa = tb >> 1, xh = tb & 1;
+  const char* xp[2];
 #pragma unroll
-        for (int s = 8; s >= 1; s >>= 1) {
-          const float ov = __shfl_xor(bv, s, 64);
-          const int oc = __shfl_xor(bc, s, 64);
-          if (ov > bv || (ov == bv && oc < bc)) { bv = ov; bc = oc; }
-        }
-        if (ok && j == 0) a.argmax_parts[m * (a.N / 16) + run] = make_int2(__float_as_int(bv), bc);
-      }
+  for (int r = 0; r < 2; ++r) xp[r] = (const char*)a.x + min(m0 + xa + 128 * r, M - 1) * a.ldx * 2;
+
+  Half wm[2][4];
+  uint32_t we[2];
+  uint4 xr[2][2][4];  // [set][row][16 bytes]
+  auto load_w = [&](int k0, int set) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int k = min(min(k0, last) + 4 * rq, K - 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wm[set][r] = *(const Half*)(mrun + (int64_t)(k + r) * RB);
+    we[set] = *(const uint32_t*)(erun + k);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto load_x = [&](int k0, int set) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int kx = min(min(k0, last) + 32 * xh, K - 32);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xr[set][r][i] = ((const uint4*)(xp[r] + (int64_t)kx * 2))[i];
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto store_w = [&](int k0, int stage, int set) {  // 4 rows x 8 columns -> 8 columns of 4 bf16; rows past K zero
+    uint16_t* Bs = (uint16_t*)(smem + stage * STAGE) + BM * GM_LD;
+    float f[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) magnitudes8(wm[set][r], f[r]);
+    const bool ok = k0 + 4 * rq < K;
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = ok ? ldexpf(1.f, (int)((we[set] >> (8 * r)) & 255u) - 133) : 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      *(uint2*)(Bs + (lr * 16 + ch * 8 + c) * GM_LD + 4 * rq) =
+          make_uint2(pack_bf16_exact(f[0][c] * sc[0], f[1][c] * sc[1]), pack_bf16_exact(f[2][c] * sc[2], f[3][c] * sc[3]));
+  };
+  auto store_x = [&](int stage, int set) {
+    uint16_t* As = (uint16_t*)(smem + stage * STAGE);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *(uint4*)(As + (xa + 128 * r) * GM_LD + 32 * xh + 8 * i) = make_uint4(xr[set][r][i].x, xr[set][r][i].y, xr[set][r][i].z, xr[set][r][i].w);
+  };
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+  const int fr = lane & 31, fk = 8 * (lane >> 5);
+  auto compute = [&](int stage) {
+    const uint16_t* As = (const uint16_t*)(smem + stage * STAGE);
+    const uint16_t* Bs = As + BM * GM_LD;
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int kk = 0; kk < GM_BK; kk += 16) {
+      bf16x8 af[2], bfr[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *(const bf16x8*)(As + (wr + 32 * i + fr) * GM_LD + kk + fk);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bfr[j] = *(const bf16x8*)(Bs + (wc + 32 * j + fr) * GM_LD + kk + fk);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
-  } else {  // the pairs: a thread a (first-half) column, 4 rows a pass
-    const int c = t & 63, p = c >> 4, j = c & 15;
-    const int64_t run = tile_run(a, tn, p);
-    const int64_t c0 = run * 16 + j;
-    for (int r = t >> 6; r < BM; r += NT / 64) {
-      const int64_t m = m0 + r;
-      if (m >= M || run < 0) continue;
-      float x0 = Cs[r * GM_LDC + c] * rs_s[r], x1 = Cs[r * GM_LDC + c + 64] * rs_s[r];
-      if (kind == FH_EP_SILU_GATE) {
-        const float sc = g.scale_rows ? g.row_w[ybase + m] : 1.f;
-        store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + c0, silu(x0) * x1 * sc);
-      } else {  // FH_EP_ROPE_KV
-        const int hd = a.head_dim;
-        const int h = (int)c0 / hd, d = (int)c0 % hd, d1 = d + hd / 2;  // (c0 < N < 2^31)
-        if (h < a.heads + a.kv_heads) {  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
-          const int64_t place = rope_place(a, a.places[m]);
-          const float* cs = a.cos_tab + place * hd;
-          const float* sn = a.sin_tab + place * hd;
-          const float t0 = x0 * cs[d] - x1 * sn[d], t1 = x1 * cs[d1] + x0 * sn[d1];
-          x0 = t0; x1 = t1;
-        }
-        if (h < a.heads) {
-          float* q = (float*)a.y + m * a.ldy + (int64_t)h * hd;
-          q[d] = x0; q[d1] = x1;
-        } else {
-          const int ch = h - a.heads;
-          cache_put(a, ch, a.cache_rows[m], d, d1, j, x0, x1);
-        }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // each row's 1 / rms from the sums of squares its maker left by runs of 16 (two threads a row)
+  auto row_scales = [&] {
+    const int ar = t >> 1, ah = t & 1;
+    const int64_t xrow = min(m0 + ar, M - 1);
+    if (a.ssq_in) {
+      float s = 0.f;
+      if (m0 + ar < M) {
+        const float* q = a.ssq_in + xrow * a.ssq_parts;
+        for (int i = ah; i < a.ssq_parts; i += 2) s += q[i];
       }
+      s += __shfl_xor(s, 1, 64);
+      if (ah == 0) rs_s[ar] = 1.0f / sqrtf(s / (float)K + a.eps);
+    } else if (ah == 0) {
+      rs_s[ar] = 1.f;
+    }
+  };
+  // Each group runs a loop of its own (the same barriers, in the same order), so that the compiler sees one group's
+  // loads alone and waits only for the set a store takes, not for the loads issued after it. Step s's operands are
+  // in stage s % 2; a pair of steps is 4 phases: [A: products of stage 0 | B: x of step s + 1 into stage 1], [A: the
+  // weight of step s + 1 into stage 1 | B: products of stage 0], then the same with the stages swapped; each store
+  // takes the register set loaded two phases of its group before, which then takes the loads of 3 steps on.
+  // (An odd count of steps ends with a step of zero weights.)
+  if (wgrp) {
+    load_w(0, 0); load_w(GM_BK, 1); store_w(0, 0, 0); load_w(2 * GM_BK, 0);
+    row_scales();
+    __syncthreads();
+    for (int s = 0; s * GM_BK < K; s += 2) {
+      compute(0);
+      __syncthreads();
+      store_w((s + 1) * GM_BK, 1, 1); load_w((s + 3) * GM_BK, 1);
+      __syncthreads();
+      compute(1);
+      __syncthreads();
+      store_w((s + 2) * GM_BK, 0, 0); load_w((s + 4) * GM_BK, 0);
+      __syncthreads();
+    }
+  } else {
+    load_x(0, 0); load_x(GM_BK, 1); store_x(0, 0); load_x(2 * GM_BK, 0);
+    row_scales();
+    __syncthreads();
+    for (int s = 0; s * GM_BK < K; s += 2) {
+      store_x(1, 1); load_x((s + 3) * GM_BK, 1);
+      __syncthreads();
+      compute(0);
+      __syncthreads();
+      store_x(0, 0); load_x((s + 4) * GM_BK, 0);
+      __syncthreads();
+      compute(1);
+      __syncthreads();
     }
   }
+
+  // the output tile, fp32, through LDS (the stages are free: the last barrier passed every wave's products)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        Cs[(wr + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * GM_LDC + wc + 32 * j + (lane & 31)] = acc[i][j][r];
+  __syncthreads();
+  gemm_epilogue<BM, NT>(a, g, Cs, rs_s, tn, m0, M, ybase, t);
 }
 
 // The tiled kernel over a's M rows (per expert, gathered, when g.counts is set: grid.y = experts)
@@ -343,7 +535,13 @@ int gemm_tiles(const MatArgs& a, const SkinnyMoe& g, int fmt, int experts, hipSt
     return n;
   }();
   const int64_t tiles_n0 = a.P == 1 ? (a.N / 16 + 7) / 8 : ((int64_t)a.items + 3) / 4;
-  const int TMv = (!g.counts && (a.M + 2 * GM_BM - 1) / (2 * GM_BM) * tiles_n0 <= cus) ? 2 : 1;
+  // gemm_pp_kernel for bf16 rows without the norm, where its 256-row tiles fill the CUs' rounds (at most one round,
+  // or the last round at least 7/8 full: qkv's 384 tiles of 2048 rows ran at 656 TFLOP/s against 712-750 for
+  // 128-row tiles two a CU)
+  const int64_t tiles2 = (a.M + 2 * GM_BM - 1) / (2 * GM_BM) * tiles_n0;
+  const bool pp = !g.counts && a.x_bf16 && !a.x_tiles && !a.norm_w &&
+                  (tiles2 <= cus || tiles2 * 8 >= (tiles2 + cus - 1) / cus * cus * 7);
+  const int TMv = (pp || (!g.counts && tiles2 <= cus)) ? 2 : 1;
   const int64_t tiles_m = (a.M + GM_BM * TMv - 1) / (GM_BM * TMv);
   const int64_t tiles_n = tiles_n0;
   if (tiles_m * tiles_n >= (1LL << 31)) return fail(FH_EUNSUP, "fh_gemm_bfp: too many tiles");
@@ -353,6 +551,11 @@ int gemm_tiles(const MatArgs& a, const SkinnyMoe& g, int fmt, int experts, hipSt
   const dim3 grid((unsigned)tiles, g.counts ? experts : 1), b(GM_THREADS * TMv);
   const int tm = (int)tiles_m, tn = (int)tiles_n;
   const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
+  if (pp) {
+    if (fmt == FH_BFP4) hipLaunchKernelGGL((gemm_pp_kernel<true>), grid, b, 0, s, a, tm, tn, g);
+    else hipLaunchKernelGGL((gemm_pp_kernel<false>), grid, b, 0, s, a, tm, tn, g);
+    return FH_OK;
+  }
 #define GM_LAUNCH(F, X, N) do { if (TMv == 2) hipLaunchKernelGGL((gemm_kernel<F, X, N, 2>), grid, b, 0, s, a, tm, tn, g); \
                                  else hipLaunchKernelGGL((gemm_kernel<F, X, N, 1>), grid, b, 0, s, a, tm, tn, g); } while (0)
   switch (which) {
