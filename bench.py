@@ -2,7 +2,7 @@
 attention and the output layer in bfp8, every MLP matrix in bfp4, a bf16 KV cache at context 2048, batch 1).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c3-bfp8|c2] [--batch B] [--no-cpu] [--no-prefill]
-                [--only bs16|prefill|moe|floor|peaks|c1|c2]
+                [--only bs1|bs16|prefill|moe|floor|peaks|c1|c2]
 
 Prints ONE JSON line: tokens/s of the whole decode step (every kernel of it replayed as one HIP graph, inputs resident
 in HBM), the dominant GEMV's achieved HBM bandwidth against the 8 TB/s peak (timed live with HIP events on its own
@@ -12,7 +12,7 @@ its own field, with the same step with every matrix bfp8 (`decode_bfp8`), batche
 `configs` holds config 1's GEMV and config 2's SmolLM step on the GPU, and the numpy CPU baselines of configs 1, 2, 4
 and 5 (bounded samples, each saying how it was scaled). Synthetic data: random-init weights, drawn on the GPU and
 packed there. --only runs one part by itself and prints its fields as the JSON line (what a profiler run of one part
-uses): the batch-16 step, config 4's prefill, config 5's MoE layer, the read floor (read_floor), the matrix cores'
+uses): the batch-1 step and its GEMVs, the batch-16 step, config 4's prefill, config 5's MoE layer, the read floor (read_floor), the matrix cores'
 and LDS's own rates (core_peaks), config 1's GEMVs or config 2's SmolLM step."""
 import argparse, json, os, statistics, sys, time
 import numpy as np
@@ -106,7 +106,8 @@ def step_rate(dec, context, steps, warmup, stream):
     b.synchronize()
   ms = a.elapsed_time(b) / steps
   nbytes = dec.weight_bytes() + c.layers * 2 * c.kv * dec.hd * context * 2
-  return {"workload": f"config 3 with every matrix bfp8: Llama-3.1-8B-shape decode, batch 1, context {context}, bf16 KV",
+  mats = "every matrix bfp8" if dec.mode == "bfp8" else "attention and output layer bfp8, MLP bfp4"
+  return {"workload": f"config 3 with {mats}: Llama-3.1-8B-shape decode, batch 1, context {context}, bf16 KV",
           "ms_per_step": round(ms, 4), "tokens_per_s": round(1000 / ms, 2), "step_bytes": nbytes,
           "step_gbs": round(nbytes / ms / 1e6, 1)}
 
@@ -280,8 +281,16 @@ def config2_rate(dev, steps=50, warmup=5, place=143):
   nbytes = dec.weight_bytes() + c.layers * 2 * c.kv * dec.hd * (place + 1) * 2
   del dec
   torch.cuda.empty_cache()
+  # the step's launches (embedding; qkv, attention, combine, o, gate_up, down a block; output layer; pick), each
+  # replaced by a one-workgroup read of 4 KiB in a graph of as many launches: what the launches alone cost
+  from ferrite_amd import lib
+  launches = 6 * c.layers + 3
+  buf, sink = torch.ones(1024, device=dev), torch.empty(64, dtype=torch.int32, device=dev)
+  floor = timed_graph(lambda: [lib.call("fh_read_probe", buf.data_ptr(), 4096, sink.data_ptr(), 1,
+                                        torch.cuda.current_stream().cuda_stream) for _ in range(launches)], 5, stream)
   return {"workload": f"config 2: SmolLM-135M-shape decode, batch 1, place {place}, bfp8, bf16 KV", "ms_per_step": round(ms, 4),
-          "tokens_per_s": round(1000 / ms, 1), "step_bytes": nbytes, "step_gbs": round(nbytes / ms / 1e6, 1)}
+          "tokens_per_s": round(1000 / ms, 1), "step_bytes": nbytes, "step_gbs": round(nbytes / ms / 1e6, 1),
+          "launches": launches, "launch_floor_ms": round(floor, 4)}
 
 
 def _median_time(fn, runs):
@@ -515,7 +524,7 @@ def main():
   ap.add_argument("--batch", type=int, default=1)
   ap.add_argument("--no-cpu", action="store_true")
   ap.add_argument("--no-prefill", action="store_true", help="skip config 4's prefill measurement")
-  ap.add_argument("--only", choices=("bs16", "prefill", "moe", "floor", "peaks", "c1", "c2"), help="run one part alone (see above)")
+  ap.add_argument("--only", choices=("bs1", "bs16", "prefill", "moe", "floor", "peaks", "c1", "c2"), help="run one part alone (see above)")
   ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                   help="first run a plain copy kernel (torch.neg) over MIB MiB: the known-size kernel that calibrates "
                        "rocprofv3's FETCH_SIZE/WRITE_SIZE counters in the same run")
@@ -536,7 +545,12 @@ def main():
     del src, dst
   c, mode, context = config(args.config)
   if args.only:
-    if args.only == "bs16":
+    if args.only == "bs1":  # the --config step at batch 1 and each of its GEMVs
+      dec = G.Decoder(c, G.random_weights(c, seed=1, device=dev), mode=mode, kv="bf16", batch=1, context=context)
+      stream = torch.cuda.Stream(device=dev)
+      r = step_rate(dec, context, args.steps, args.warmup, stream)
+      r["gemv"] = {k: {"us": round(v["us"], 2), "gbs": round(v["gbs"], 1)} for k, v in gemv_rates(dec, stream).items()}
+    elif args.only == "bs16":
       dec = G.Decoder(c, G.random_weights(c, seed=1, device=dev), mode=mode, kv="bf16", batch=1, context=context)
       r = decode_batch(dec, context)
     elif args.only == "prefill": r = prefill_rate()
