@@ -4,7 +4,8 @@
 // A workgroup takes one item (one run of 16 columns, or two paired runs: RoPE's halves of a head, SwiGLU's gate and up)
 // and its W waves split the K rows into W slices. A lane takes one row k of a run at a time: one 16-byte load of the
 // 16 magnitudes (8 bytes for bfp4), the exponent byte and the row's x values, then for each batch row x scaled by the
-// block's 2^(e - 133) (exact) and 16 FMAs, each magnitude converted by one sign-extending byte convert. A wave's 64
+// block's 2^(e - 133) (exact) and 16 FMAs, each bfp8 magnitude converted by one sign-extending byte convert (bfp4's
+// two a conversion through the fp8 converter, offset by 8: magnitudes_off8). A wave's 64
 // lanes read 64 consecutive rows, 1 KiB contiguous (512 B for bfp4), and keep U such loads in flight. The lanes'
 // partial sums are reduced across the wave by lane swaps and DPP moves (no LDS), across the waves through LDS in a
 // fixed order (results do not depend on timing), and the epilogue runs on the workgroup's outputs. Few registers
