@@ -39,90 +39,129 @@ __device__ inline uint32_t pack_bf16_exact(float lo, float hi) {  // both exact 
 }
 __device__ inline uint32_t pack_bf16_rne(float lo, float hi) { return bf16_rne_f(lo) | (bf16_rne_f(hi) << 16); }
 
-// the run a tile's local run lr (0..7) stands for, or -1 past the weight
+// the run a tile's local run lr (0 .. RUNS - 1) stands for, or -1 past the weight: RUNS runs of 16 columns a tile, or
+// RUNS / 2 pairs (the first runs, then their partners)
+template <int RUNS = 8>
 __device__ inline int64_t tile_run(const MatArgs& a, int tn, int lr) {
   if (a.P == 1) {
-    const int64_t nb = (int64_t)tn * 8 + lr;
+    const int64_t nb = (int64_t)tn * RUNS + lr;
     return nb < a.N / 16 ? nb : -1;
   }
-  const int64_t it = (int64_t)tn * 4 + (lr & 3);
+  const int64_t it = (int64_t)tn * (RUNS / 2) + lr % (RUNS / 2);
   if (it >= a.items) return -1;
   const int64_t nb0 = pair_first(it, a.pair_half);
-  return lr < 4 ? nb0 : nb0 + a.pair_half;
+  return lr < RUNS / 2 ? nb0 : nb0 + a.pair_half;
 }
 
-// The tile's epilogue: every output of the fp32 tile Cs [BM][GM_LDC] (staged in LDS: each output sees its row's 1/rms
-// and its pair partner, whichever wave computed it) through a's epilogue, NT threads
-template <int BM, int NT>
+// The tile's epilogue: every output of the fp32 tile Cs [BM][BN + 4] (staged in LDS: each output sees its row's 1/rms
+// and its pair partner, whichever wave computed it) through a's epilogue, NT threads (those of whole passes over the
+// tile's columns: NT / BN of them a pass, the rest idle; a pass's threads start at a multiple of 64, so a run's 16
+// columns are 16 lanes of one wave)
+template <int BM, int NT, int BN = 128>
 __device__ inline void gemm_epilogue(const MatArgs& a, const SkinnyMoe& g, const float* Cs, const float* rs_s, int tn,
                                      int64_t m0, int64_t M, int64_t ybase, int t) {
+  constexpr int LDC = BN + 4, RUNS = BN / 16, H = BN / 2;
   const int kind = a.kind;
   if (a.P == 1 && kind == FH_EP_PROGRAM) {  // (a loop of its own: the program's decoding, hoisted out of the loop,
                                             // runs only here)
-    const int c = t & 127;
-    const int64_t run = tile_run(a, tn, c >> 4);
+    if (t >= NT / BN * BN) return;
+    const int c = t % BN;
+    const int64_t run = tile_run<RUNS>(a, tn, c >> 4);
     const int64_t col = run * 16 + (c & 15);
-    for (int r = t >> 7; r < BM; r += NT / 128) {
+    for (int r = t / BN; r < BM; r += NT / BN) {
       const int64_t m = m0 + r;
       if (m < M && run >= 0)
-        store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + col, prog_eval(a.prog, Cs[r * GM_LDC + c] * rs_s[r], 0, m, col));
+        store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + col, prog_eval(a.prog, Cs[r * LDC + c] * rs_s[r], 0, m, col));
     }
-  } else if (a.P == 1) {  // FH_EP_STORE, FH_EP_RESIDUAL: a thread a column, 2 rows a pass; a run is 16 lanes
-    const int c = t & 127, j = c & 15;
-    const int64_t run = tile_run(a, tn, c >> 4);
+  } else if (a.P == 1) {  // FH_EP_STORE, FH_EP_RESIDUAL: a thread a column, NT / BN rows a pass; a run is 16 lanes
+    if (t >= NT / BN * BN) return;
+    const int c = t % BN, j = c & 15;
+    const int64_t run = tile_run<RUNS>(a, tn, c >> 4);
     const int64_t col = run * 16 + j;
-    for (int r = t >> 7; r < BM; r += NT / 128) {
-      const int64_t m = m0 + r;
-      const bool ok = m < M && run >= 0;
-      const int64_t at = (ybase + m) * a.ldy + col;
-      float v = Cs[r * GM_LDC + c] * rs_s[r];
-      if (kind == FH_EP_RESIDUAL && ok) v += a.residual[at];
-      if (ok) store_out(a.y, a.y_bf16, at, v);
-      if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) put_copy(a, m, col, v);
-      if (kind == FH_EP_RESIDUAL && a.ssq_out) {
-        float s = v * v;
-        s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
-        if (ok && j == 0) a.ssq_out[m * (a.N / 16) + run] = s;
-      }
-      if (kind == FH_EP_STORE && a.argmax_parts) {
-        float bv = v;
-        int bc = (int)col;
+    // rows in batches of RB, the batch's residual loads issued together before its stores (one loop iteration a row
+    // would wait for each load in turn: the stores may alias them, so nothing moves a load above the store before it)
+    constexpr int S = NT / BN, RB = 8;
+    for (int rb = t / BN; rb < BM; rb += RB * S) {
+      float res[RB];
 #pragma unroll
-        for (int s = 8; s >= 1; s >>= 1) {
-          const float ov = __shfl_xor(bv, s, 64);
-          const int oc = __shfl_xor(bc, s, 64);
-          if (ov > bv || (ov == bv && oc < bc)) { bv = ov; bc = oc; }
+      for (int u = 0; u < RB; ++u) {
+        const int64_t m = min(m0 + rb + u * S, M - 1);
+        res[u] = (kind == FH_EP_RESIDUAL && run >= 0) ? a.residual[(ybase + m) * a.ldy + col] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const int r = rb + u * S;
+        if (r >= BM) continue;  // (the same for a wave's lanes)
+        const int64_t m = m0 + r;
+        const bool ok = m < M && run >= 0;
+        const int64_t at = (ybase + m) * a.ldy + col;
+        float v = Cs[r * LDC + c] * rs_s[r];
+        if (kind == FH_EP_RESIDUAL) v += res[u];
+        if (ok) store_out(a.y, a.y_bf16, at, v);
+        if (kind == FH_EP_RESIDUAL && a.copy_bf16 && ok) put_copy(a, m, col, v);
+        if (kind == FH_EP_RESIDUAL && a.ssq_out) {
+          float s = v * v;
+          s += __shfl_xor(s, 8, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 1, 64);
+          if (ok && j == 0) a.ssq_out[m * (a.N / 16) + run] = s;
         }
-        if (ok && j == 0) a.argmax_parts[m * (a.N / 16) + run] = make_int2(__float_as_int(bv), bc);
+        if (kind == FH_EP_STORE && a.argmax_parts) {
+          float bv = v;
+          int bc = (int)col;
+#pragma unroll
+          for (int s = 8; s >= 1; s >>= 1) {
+            const float ov = __shfl_xor(bv, s, 64);
+            const int oc = __shfl_xor(bc, s, 64);
+            if (ov > bv || (ov == bv && oc < bc)) { bv = ov; bc = oc; }
+          }
+          if (ok && j == 0) a.argmax_parts[m * (a.N / 16) + run] = make_int2(__float_as_int(bv), bc);
+        }
       }
     }
-  } else {  // the pairs: a thread a (first-half) column, 4 rows a pass
-    const int c = t & 63, p = c >> 4, j = c & 15;
-    const int64_t run = tile_run(a, tn, p);
+  } else {  // the pairs: a thread a (first-half) column, NT / H rows a pass, in batches of RB rows (their loads first)
+    if (t >= NT / H * H) return;
+    const int c = t % H, p = c >> 4, j = c & 15;
+    const int64_t run = tile_run<RUNS>(a, tn, p);
     const int64_t c0 = run * 16 + j;
-    for (int r = t >> 6; r < BM; r += NT / 64) {
-      const int64_t m = m0 + r;
-      if (m >= M || run < 0) continue;
-      float x0 = Cs[r * GM_LDC + c] * rs_s[r], x1 = Cs[r * GM_LDC + c + 64] * rs_s[r];
-      if (kind == FH_EP_SILU_GATE) {
-        const float sc = g.scale_rows ? g.row_w[ybase + m] : 1.f;
-        store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + c0, silu(x0) * x1 * sc);
-      } else {  // FH_EP_ROPE_KV
-        const int hd = a.head_dim;
-        const int h = (int)c0 / hd, d = (int)c0 % hd, d1 = d + hd / 2;  // (c0 < N < 2^31)
-        if (h < a.heads + a.kv_heads) {  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
+    const bool rope = kind == FH_EP_ROPE_KV;
+    const int hd = rope ? a.head_dim : 1;
+    const int h = (int)c0 / hd, d = (int)c0 % hd, d1 = d + hd / 2;  // (c0 < N < 2^31)
+    const bool turn = rope && h < a.heads + a.kv_heads;  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
+    constexpr int S = NT / H, RB = 4;
+    for (int rb = t / H; rb < BM; rb += RB * S) {
+      float cs0[RB], cs1[RB], sn0[RB], sn1[RB], sc[RB];
+      int32_t crow[RB];
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {  // the batch's per-row loads: the row's weight, or its place's table rows
+        const int64_t m = min(m0 + rb + u * S, M - 1);
+        sc[u] = (!rope && g.scale_rows) ? g.row_w[ybase + m] : 1.f;
+        crow[u] = rope && h >= a.heads ? a.cache_rows[m] : 0;
+        cs0[u] = cs1[u] = 1.f;
+        sn0[u] = sn1[u] = 0.f;
+        if (turn) {
           const int64_t place = rope_place(a, a.places[m]);
-          const float* cs = a.cos_tab + place * hd;
-          const float* sn = a.sin_tab + place * hd;
-          const float t0 = x0 * cs[d] - x1 * sn[d], t1 = x1 * cs[d1] + x0 * sn[d1];
-          x0 = t0; x1 = t1;
+          cs0[u] = a.cos_tab[place * hd + d]; cs1[u] = a.cos_tab[place * hd + d1];
+          sn0[u] = a.sin_tab[place * hd + d]; sn1[u] = a.sin_tab[place * hd + d1];
         }
-        if (h < a.heads) {
-          float* q = (float*)a.y + m * a.ldy + (int64_t)h * hd;
-          q[d] = x0; q[d1] = x1;
+      }
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const int r = rb + u * S;
+        const int64_t m = m0 + r;
+        if (r >= BM || m >= M || run < 0) continue;
+        float x0 = Cs[r * LDC + c] * rs_s[r], x1 = Cs[r * LDC + c + H] * rs_s[r];
+        if (!rope) {  // FH_EP_SILU_GATE
+          store_out(a.y, a.y_bf16, (ybase + m) * a.ldy + c0, silu(x0) * x1 * sc[u]);
         } else {
-          const int ch = h - a.heads;
-          cache_put(a, ch, a.cache_rows[m], d, d1, j, x0, x1);
+          if (turn) {
+            const float t0 = x0 * cs0[u] - x1 * sn0[u], t1 = x1 * cs1[u] + x0 * sn1[u];
+            x0 = t0; x1 = t1;
+          }
+          if (h < a.heads) {
+            float* q = (float*)a.y + m * a.ldy + (int64_t)h * hd;
+            q[d] = x0; q[d1] = x1;
+          } else {
+            cache_put(a, h - a.heads, crow[u], d, d1, j, x0, x1);
+          }
         }
       }
     }
@@ -341,24 +380,28 @@ __global__ __launch_bounds__(GM_THREADS * TM, 3 - TM) void gemm_kernel(MatArgs a
 }
 
 // The same GEMM in the two-group ("ping-pong") form, for bf16 rows with no RMSNorm prologue (a prompt's matmuls: their
-// x rows come normalised, as bf16, from fh_rms_rows, attention or SwiGLU): a workgroup of 8 waves takes a 256 x 128
-// tile, each wave a 64 x 64 quarter of a 128-row half as gemm_kernel's waves do; waves 0-3 (one a SIMD) load and
-// convert the weight, waves 4-7 (the other one a SIMD) load and copy x's rows. A K step is two phases between
-// workgroup barriers: in the first, waves 0-3 run their products on the step's LDS stage while waves 4-7 write the
-// next step's x into the other stage; in the second, waves 4-7 run their products while waves 0-3 write the next
-// step's weight. So on each SIMD one wave keeps the matrix core busy while the other does the loads, the conversion
-// and the LDS writes, and the products' wave has the higher issue priority (s_setprio). Global loads run two steps
-// ahead, in two register sets. The results are gemm_kernel's bit for bit (the same products in the same order).
-// Measured at 2048 rows of the 8B shapes against gemm_kernel in the same run: o 739 -> 796, gate_up 803 -> 842,
-// down 826 -> 922 TFLOP/s.
-template <bool FOUR>
+// x rows come normalised, as bf16, from fh_rms_rows, attention or SwiGLU): a workgroup of 8 waves takes a 256 x BN
+// tile (BN = 64 WN: 128, 192 or 256 columns, 4 WN runs of 16 or 2 WN pairs), each wave 64 rows x 32 WN columns; waves
+// 0-3 (one a SIMD) load and convert the weight, waves 4-7 (the other one a SIMD) load and copy x's rows. A K step is
+// two phases between workgroup barriers: in the first, waves 0-3 run their products on the step's LDS stage while
+// waves 4-7 write the next step's x into the other stage; in the second, waves 4-7 run their products while waves 0-3
+// write the next step's weight. So on each SIMD one wave keeps the matrix core busy while the other does the loads,
+// the conversion and the LDS writes, and the products' wave has the higher issue priority (s_setprio). Global loads
+// run two steps ahead, in two register sets. The products are gemm_kernel's in the same order, so the results are its
+// bit for bit. Measured at 2048 rows of the 8B shapes against gemm_kernel in the same run (128 columns): o 739 -> 796,
+// gate_up 803 -> 842, down 826 -> 922 TFLOP/s. A tile wider than 128 columns stages its fp32 output in two halves of
+// 128 rows (its whole would not fit in LDS).
+template <bool FOUR, int WN>
 __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, int tiles_m, int tiles_n, SkinnyMoe g) {
-  constexpr int BM = 2 * GM_BM, NT = 2 * GM_THREADS;
-  constexpr int STAGE = (BM + GM_BN) * GM_LD * 2;
-  constexpr int LDS = 2 * STAGE > BM * GM_LDC * 4 ? 2 * STAGE : BM * GM_LDC * 4;
+  constexpr int BM = 2 * GM_BM, NT = 2 * GM_THREADS, BN = 64 * WN, RUNS = 4 * WN, LDC = BN + 4;
+  constexpr int STAGE = (BM + BN) * GM_LD * 2;
+  constexpr bool ONE_PASS = BM * LDC * 4 <= 150 * 1024;  // the whole output tile in LDS at once
+  constexpr int CROWS = ONE_PASS ? BM : BM / 2;           // rows of the output tile a pass
+  constexpr int LDS = 2 * STAGE > CROWS * LDC * 4 ? 2 * STAGE : CROWS * LDC * 4;
+  constexpr int UPT = (RUNS + 7) / 8;  // the weight's units (8 columns x 4 rows of a step) a thread: 32 RUNS in all
   __shared__ __attribute__((aligned(16))) char smem[LDS];
   __shared__ float rs_s[BM];
-  float* Cs = (float*)smem;  // [256][132]: the output tile (after the K loop)
+  float* Cs = (float*)smem;  // [CROWS][BN + 4]: the output tile (after the K loop)
 
   const int64_t M = a.M, ybase = 0;
   int id = blockIdx.x;
@@ -376,11 +419,22 @@ __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, i
   constexpr int RB = FOUR ? 8 : 16;
   using Half = typename std::conditional<FOUR, uint32_t, uint2>::type;  // 8 of a row's 16 magnitudes
 
-  // the weight's threads (0-255): run lr (of 8), rows 4 rq .. 4 rq + 3, columns 8 ch .. 8 ch + 7
-  const int lr = (t >> 5) & 7, rq = (t & 31) >> 1, ch = t & 1;
-  const int64_t nb = tile_run(a, tn, lr);
-  const uint8_t* mrun = a.mant + (nb < 0 ? 0 : nb) * a.K * RB + ch * (RB / 2);
-  const uint8_t* erun = a.exps + (nb < 0 ? 0 : nb) * a.K;
+  // the weight's threads (0-255): unit t + 256 i is run lr_i = (t >> 5) + 8 i, rows 4 rq .. 4 rq + 3, columns
+  // 8 ch .. 8 ch + 7 of the run (a wave's 32-lane halves write 8 columns apart: no LDS bank in common); a unit past the
+  // tile's runs (12 runs: the second unit of threads 128-255) is skipped, a whole wave at a time
+  const int rq = (t & 31) >> 1, ch = t & 1;
+  int lr[UPT];
+  bool uok[UPT];
+  const uint8_t* mrun[UPT];
+  const uint8_t* erun[UPT];
+#pragma unroll
+  for (int i = 0; i < UPT; ++i) {
+    lr[i] = ((t >> 5) & 7) + 8 * i;
+    uok[i] = lr[i] < RUNS;
+    const int64_t nb = uok[i] ? tile_run<RUNS>(a, tn, lr[i]) : -1;
+    mrun[i] = a.mant + (nb < 0 ? 0 : nb) * a.K * RB + ch * (RB / 2);
+    erun[i] = a.exps + (nb < 0 ? 0 : nb) * a.K;
+  }
   // x's threads (256-511): rows xa and xa + 128 of the tile, k half xh (32 values, 4 x 16 bytes each)
   // (a row's two halves in neighbouring lanes: 16 lanes over 16 rows of one half write LDS without bank conflicts
   // but load 16 lines where these load 8, and measured slower: o 796 -> 743, gate_up 842 -> 772 TFLOP/s)
@@ -389,15 +443,19 @@ __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, i
 #pragma unroll
   for (int r = 0; r < 2; ++r) xp[r] = (const char*)a.x + min(m0 + xa + 128 * r, M - 1) * a.ldx * 2;
 
-  Half wm[2][4];
-  uint32_t we[2];
+  Half wm[2][UPT][4];
+  uint32_t we[2][UPT];
   uint4 xr[2][2][4];  // [set][row][16 bytes]
   auto load_w = [&](int k0, int set) {
     __builtin_amdgcn_sched_barrier(0);
     const int k = min(min(k0, last) + 4 * rq, K - 4);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) wm[set][r] = *(const Half*)(mrun + (int64_t)(k + r) * RB);
-    we[set] = *(const uint32_t*)(erun + k);
+    for (int i = 0; i < UPT; ++i) {
+      if (!uok[i]) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) wm[set][i][r] = *(const Half*)(mrun[i] + (int64_t)(k + r) * RB);
+      we[set][i] = *(const uint32_t*)(erun[i] + k);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
   auto load_x = [&](int k0, int set) {
@@ -409,19 +467,23 @@ __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, i
       for (int i = 0; i < 4; ++i) xr[set][r][i] = ((const uint4*)(xp[r] + (int64_t)kx * 2))[i];
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto store_w = [&](int k0, int stage, int set) {  // 4 rows x 8 columns -> 8 columns of 4 bf16; rows past K zero
+  auto store_w = [&](int k0, int stage, int set) {  // a unit's 4 rows x 8 columns -> 8 columns of 4 bf16; rows past K 0
     uint16_t* Bs = (uint16_t*)(smem + stage * STAGE) + BM * GM_LD;
-    float f[4][8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) magnitudes8(wm[set][r], f[r]);
     const bool ok = k0 + 4 * rq < K;
-    float sc[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = ok ? ldexpf(1.f, (int)((we[set] >> (8 * r)) & 255u) - 133) : 0.f;
+    for (int i = 0; i < UPT; ++i) {
+      if (!uok[i]) continue;
+      float f[4][8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
-      *(uint2*)(Bs + (lr * 16 + ch * 8 + c) * GM_LD + 4 * rq) =
-          make_uint2(pack_bf16_exact(f[0][c] * sc[0], f[1][c] * sc[1]), pack_bf16_exact(f[2][c] * sc[2], f[3][c] * sc[3]));
+      for (int r = 0; r < 4; ++r) magnitudes8(wm[set][i][r], f[r]);
+      float sc[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = ok ? ldexpf(1.f, (int)((we[set][i] >> (8 * r)) & 255u) - 133) : 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        *(uint2*)(Bs + (lr[i] * 16 + ch * 8 + c) * GM_LD + 4 * rq) =
+            make_uint2(pack_bf16_exact(f[0][c] * sc[0], f[1][c] * sc[1]), pack_bf16_exact(f[2][c] * sc[2], f[3][c] * sc[3]));
+    }
   };
   auto store_x = [&](int stage, int set) {
     uint16_t* As = (uint16_t*)(smem + stage * STAGE);
@@ -432,14 +494,14 @@ __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, i
         *(uint4*)(As + (xa + 128 * r) * GM_LD + 32 * xh + 8 * i) = make_uint4(xr[set][r][i].x, xr[set][r][i].y, xr[set][r][i].z, xr[set][r][i].w);
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[2][WN];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 32 * WN;
   const int fr = lane & 31, fk = 8 * (lane >> 5);
   auto compute = [&](int stage) {
     const uint16_t* As = (const uint16_t*)(smem + stage * STAGE);
@@ -447,15 +509,15 @@ __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, i
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kk = 0; kk < GM_BK; kk += 16) {
-      bf16x8 af[2], bfr[2];
+      bf16x8 af[2], bfr[WN];
 #pragma unroll
       for (int i = 0; i < 2; ++i) af[i] = *(const bf16x8*)(As + (wr + 32 * i + fr) * GM_LD + kk + fk);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bfr[j] = *(const bf16x8*)(Bs + (wc + 32 * j + fr) * GM_LD + kk + fk);
+      for (int j = 0; j < WN; ++j) bfr[j] = *(const bf16x8*)(Bs + (wc + 32 * j + fr) * GM_LD + kk + fk);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
     __builtin_amdgcn_s_setprio(0);
   };
@@ -512,16 +574,23 @@ __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, i
     }
   }
 
-  // the output tile, fp32, through LDS (the stages are free: the last barrier passed every wave's products)
+  // the output tile, fp32, through LDS (the stages are free: the last barrier passed every wave's products), in one
+  // pass or in two of 128 rows (waves 0-3's rows, then 4-7's)
+  for (int h = 0; h < BM / CROWS; ++h) {
+    if (ONE_PASS || (wave >> 2) == h) {
+      const int r0 = wr - h * CROWS;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        Cs[(wr + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * GM_LDC + wc + 32 * j + (lane & 31)] = acc[i][j][r];
-  __syncthreads();
-  gemm_epilogue<BM, NT>(a, g, Cs, rs_s, tn, m0, M, ybase, t);
+          for (int r = 0; r < 16; ++r)
+            Cs[(r0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LDC + wc + 32 * j + (lane & 31)] = acc[i][j][r];
+    }
+    __syncthreads();
+    gemm_epilogue<CROWS, NT, BN>(a, g, Cs, rs_s + h * CROWS, tn, m0 + h * CROWS, M, ybase, t);
+    if (h + 1 < BM / CROWS) __syncthreads();  // (the next pass rewrites Cs)
+  }
 }
 
 // The tiled kernel over a's M rows (per expert, gathered, when g.counts is set: grid.y = experts)
@@ -535,12 +604,23 @@ int gemm_tiles(const MatArgs& a, const SkinnyMoe& g, int fmt, int experts, hipSt
     return n;
   }();
   const int64_t tiles_n0 = a.P == 1 ? (a.N / 16 + 7) / 8 : ((int64_t)a.items + 3) / 4;
-  // gemm_pp_kernel for bf16 rows without the norm, where its 256-row tiles fill the CUs' rounds (at most one round,
-  // or the last round at least 7/8 full: qkv's 384 tiles of 2048 rows ran at 656 TFLOP/s against 712-750 for
-  // 128-row tiles two a CU)
   const int64_t tiles2 = (a.M + 2 * GM_BM - 1) / (2 * GM_BM) * tiles_n0;
-  const bool pp = !g.counts && a.x_bf16 && !a.x_tiles && !a.norm_w &&
-                  (tiles2 <= cus || tiles2 * 8 >= (tiles2 + cus - 1) / cus * cus * 7);
+  // gemm_pp_kernel for bf16 rows without the norm, its 256-row tiles 128, 192 or 256 columns wide: the widest whose
+  // tiles fill the CUs' rounds (at most one round, or the last at least 7/8 full) and no narrower tile takes fewer
+  // rounds of as much work; none filling them, the 4-wave kernel (qkv's 384 tiles of 2048 rows x 128 columns ran at
+  // 656 TFLOP/s against 712-750 for 128-row tiles two a CU)
+  int WNv = 0;
+  if (!g.counts && a.x_bf16 && !a.x_tiles && !a.norm_w) {
+    const int64_t mt = (a.M + 2 * GM_BM - 1) / (2 * GM_BM);
+    int64_t best = 0;
+    for (int wn = 2; wn <= 4; ++wn) {
+      const int64_t tiles = mt * (a.P == 1 ? (a.N / 16 + 4 * wn - 1) / (4 * wn) : ((int64_t)a.items + 2 * wn - 1) / (2 * wn));
+      const int64_t rounds = (tiles + cus - 1) / cus;
+      const bool fills = tiles <= cus || tiles * 8 >= rounds * cus * 7;
+      if (fills && (best == 0 || rounds * wn <= best)) { WNv = wn; best = rounds * wn; }
+    }
+  }
+  const bool pp = WNv != 0;
   const int TMv = (pp || (!g.counts && tiles2 <= cus)) ? 2 : 1;
   const int64_t tiles_m = (a.M + GM_BM * TMv - 1) / (GM_BM * TMv);
   const int64_t tiles_n = tiles_n0;
@@ -552,8 +632,15 @@ int gemm_tiles(const MatArgs& a, const SkinnyMoe& g, int fmt, int experts, hipSt
   const int tm = (int)tiles_m, tn = (int)tiles_n;
   const int which = (fmt == FH_BFP4) * 4 + a.x_bf16 * 2 + (a.norm_w != nullptr);
   if (pp) {
-    if (fmt == FH_BFP4) hipLaunchKernelGGL((gemm_pp_kernel<true>), grid, b, 0, s, a, tm, tn, g);
-    else hipLaunchKernelGGL((gemm_pp_kernel<false>), grid, b, 0, s, a, tm, tn, g);
+    const int64_t tnw = a.P == 1 ? (a.N / 16 + 4 * WNv - 1) / (4 * WNv) : ((int64_t)a.items + 2 * WNv - 1) / (2 * WNv);
+    const dim3 gridw((unsigned)(tiles_m * tnw));
+    const int tnv = (int)tnw;
+#define GM_PP(F) do { if (WNv == 2) hipLaunchKernelGGL((gemm_pp_kernel<F, 2>), gridw, b, 0, s, a, tm, tnv, g); \
+                      else if (WNv == 3) hipLaunchKernelGGL((gemm_pp_kernel<F, 3>), gridw, b, 0, s, a, tm, tnv, g); \
+                      else hipLaunchKernelGGL((gemm_pp_kernel<F, 4>), gridw, b, 0, s, a, tm, tnv, g); } while (0)
+    if (fmt == FH_BFP4) GM_PP(true);
+    else GM_PP(false);
+#undef GM_PP
     return FH_OK;
   }
 #define GM_LAUNCH(F, X, N) do { if (TMv == 2) hipLaunchKernelGGL((gemm_kernel<F, X, N, 2>), grid, b, 0, s, a, tm, tn, g); \

@@ -177,6 +177,35 @@ def test_gemm_epilogues(cuda, M):
     assert not got[:, mask].any(), "only the rows' cache rows written"
 
 
+@pytest.mark.parametrize("N,pairs", [(33600, False), (51200, False), (35200, True), (51200, True)])
+def test_gemm_wide_tiles(cuda, N, pairs):
+  # the two-group kernel's 192- and 256-column tiles: on an MI355X's 256 CUs, 200 rows by 2100 runs (33600) or 1100
+  # SwiGLU pairs (35200) take 192-column tiles, 3200 runs or 1600 pairs (51200) 256-column ones (the narrower tiles
+  # would need a second round they do not fill). bf16 rows against the same values as fp32 rows, which the 4-wave
+  # kernel takes (the same products in the same order: bit for bit), and against the oracle on the first and last
+  # 1024 columns (or pairs); K = 192, three steps (an odd count: a last step of zero weights)
+  L = lib()
+  rng = np.random.default_rng(16)
+  M, K = 200, 192
+  w = rng.normal(0, 0.02, (K, N)).astype(np.float32)
+  x = O.bf16(rng.normal(0, 1, (M, K)))
+  bw = ops().pack(to_gpu(w))
+  ep = (lambda: ops().epilogue(L.EP_SILU_GATE, split=N // 2)) if pairs else (lambda: None)
+  a = ops().gemm(to_gpu(x, torch.bfloat16), bw, ep())
+  b = ops().gemm(to_gpu(x), bw, ep())
+  assert torch.equal(a, b), float((a - b).abs().max())
+  y, xb = a.cpu().numpy(), x.astype(np.float64)
+  cols = np.r_[0:1024, y.shape[1] - 1024:y.shape[1]]
+  if pairs:
+    h = N // 2
+    g, u = xb @ O.bfp(w[:, cols]), xb @ O.bfp(w[:, h + cols])
+    bound = 1e-5 * (np.abs(xb) @ np.abs(O.bfp(w[:, cols]))) * (1 + np.abs(u)) + 1e-6
+    within(y[:, cols], OL.glu(g, u), bound, ("silu", N))
+  else:
+    wv = O.bfp(w[:, cols])
+    within(y[:, cols], xb @ wv, 1e-5 * (np.abs(xb) @ np.abs(wv)) + 1e-30, ("store", N))
+
+
 def test_gemm_agrees_with_gemv(cuda):
   # on rows already in bf16, the matrix cores and the exact-product GEMV differ by summation order only
   rng = np.random.default_rng(14)
