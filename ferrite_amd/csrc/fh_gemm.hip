@@ -53,13 +53,21 @@ __device__ inline int64_t tile_run(const MatArgs& a, int tn, int lr) {
   return lr < RUNS / 2 ? nb0 : nb0 + a.pair_half;
 }
 
+// RoPE's per-row values for the epilogue, staged in LDS while the tile's first loads are in flight: row ar's place and
+// cache row (m: the row, clamped into the matrix)
+__device__ inline void stage_rope_rows(const MatArgs& a, int32_t* rows_s, int bm, int ar, int64_t m) {
+  rows_s[ar] = a.places[m];
+  rows_s[bm + ar] = a.cache_rows[m];
+}
+
 // The tile's epilogue: every output of the fp32 tile Cs [BM][BN + 4] (staged in LDS: each output sees its row's 1/rms
 // and its pair partner, whichever wave computed it) through a's epilogue, NT threads (those of whole passes over the
 // tile's columns: NT / BN of them a pass, the rest idle; a pass's threads start at a multiple of 64, so a run's 16
 // columns are 16 lanes of one wave)
 template <int BM, int NT, int BN = 128>
 __device__ inline void gemm_epilogue(const MatArgs& a, const SkinnyMoe& g, const float* Cs, const float* rs_s, int tn,
-                                     int64_t m0, int64_t M, int64_t ybase, int t) {
+                                     int64_t m0, int64_t M, int64_t ybase, int t, const int32_t* place_s,
+                                     const int32_t* crow_s) {
   constexpr int LDC = BN + 4, RUNS = BN / 16, H = BN / 2;
   const int kind = a.kind;
   if (a.P == 1 && kind == FH_EP_PROGRAM) {  // (a loop of its own: the program's decoding, hoisted out of the loop,
@@ -117,7 +125,8 @@ __device__ inline void gemm_epilogue(const MatArgs& a, const SkinnyMoe& g, const
         }
       }
     }
-  } else {  // the pairs: a thread a (first-half) column, NT / H rows a pass, in batches of RB rows (their loads first)
+  } else {  // the pairs: a thread a (first-half) column, NT / H rows a pass, in batches of RB rows (their loads first;
+            // RoPE's places and cache rows staged in LDS by the kernel: place_s[r], crow_s[r] for the tile's row r)
     if (t >= NT / H * H) return;
     const int c = t % H, p = c >> 4, j = c & 15;
     const int64_t run = tile_run<RUNS>(a, tn, p);
@@ -126,19 +135,18 @@ __device__ inline void gemm_epilogue(const MatArgs& a, const SkinnyMoe& g, const
     const int hd = rope ? a.head_dim : 1;
     const int h = (int)c0 / hd, d = (int)c0 % hd, d1 = d + hd / 2;  // (c0 < N < 2^31)
     const bool turn = rope && h < a.heads + a.kv_heads;  // q's and k's heads turn: x cos + (-x2, x1) sin (models/llama.py:92-93)
-    constexpr int S = NT / H, RB = 4;
+    constexpr int S = NT / H, RB = 8;
     for (int rb = t / H; rb < BM; rb += RB * S) {
       float cs0[RB], cs1[RB], sn0[RB], sn1[RB], sc[RB];
-      int32_t crow[RB];
 #pragma unroll
       for (int u = 0; u < RB; ++u) {  // the batch's per-row loads: the row's weight, or its place's table rows
-        const int64_t m = min(m0 + rb + u * S, M - 1);
+        const int r = min(rb + u * S, BM - 1);
+        const int64_t m = min(m0 + r, M - 1);
         sc[u] = (!rope && g.scale_rows) ? g.row_w[ybase + m] : 1.f;
-        crow[u] = rope && h >= a.heads ? a.cache_rows[m] : 0;
         cs0[u] = cs1[u] = 1.f;
         sn0[u] = sn1[u] = 0.f;
         if (turn) {
-          const int64_t place = rope_place(a, a.places[m]);
+          const int64_t place = rope_place(a, place_s[r]);
           cs0[u] = a.cos_tab[place * hd + d]; cs1[u] = a.cos_tab[place * hd + d1];
           sn0[u] = a.sin_tab[place * hd + d]; sn1[u] = a.sin_tab[place * hd + d1];
         }
@@ -160,7 +168,7 @@ __device__ inline void gemm_epilogue(const MatArgs& a, const SkinnyMoe& g, const
             float* q = (float*)a.y + m * a.ldy + (int64_t)h * hd;
             q[d] = x0; q[d1] = x1;
           } else {
-            cache_put(a, h - a.heads, crow[u], d, d1, j, x0, x1);
+            cache_put(a, h - a.heads, crow_s[r], d, d1, j, x0, x1);
           }
         }
       }
@@ -175,6 +183,7 @@ __global__ __launch_bounds__(GM_THREADS * TM, 3 - TM) void gemm_kernel(MatArgs a
   constexpr int LDS = 2 * STAGE > BM * GM_LDC * 4 ? 2 * STAGE : BM * GM_LDC * 4;
   __shared__ __attribute__((aligned(16))) char smem[LDS];
   __shared__ float rs_s[BM];
+  __shared__ int32_t rows_s[2 * BM];  // (RoPE) the tile's rows' places, then their cache rows
   // stage s: x at smem + s * STAGE ([BM rows][72] bf16), W after it ([128 columns][72] bf16, K-contiguous); the fp32
   // output tile [BM][132] aliases them after the K loop
   float* Cs = (float*)smem;                            // [128][132]: the output tile (after the K loop)
@@ -323,6 +332,7 @@ __global__ __launch_bounds__(GM_THREADS * TM, 3 - TM) void gemm_kernel(MatArgs a
   } else if (ah == 0) {
     rs_s[ar] = 1.f;
   }
+  if (a.kind == FH_EP_ROPE_KV && ah == 1) stage_rope_rows(a, rows_s, BM, ar, xr0);
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -376,7 +386,7 @@ __global__ __launch_bounds__(GM_THREADS * TM, 3 - TM) void gemm_kernel(MatArgs a
         Cs[(wr + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * GM_LDC + wc + 32 * j + (lane & 31)] = acc[i][j][r];
   __syncthreads();
 
-  gemm_epilogue<BM, NT>(a, g, Cs, rs_s, tn, m0, M, ybase, t);
+  gemm_epilogue<BM, NT>(a, g, Cs, rs_s, tn, m0, M, ybase, t, rows_s, rows_s + BM);
 }
 
 // The same GEMM in the two-group ("ping-pong") form, for bf16 rows with no RMSNorm prologue (a prompt's matmuls: their
@@ -401,6 +411,7 @@ __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, i
   constexpr int UPT = (RUNS + 7) / 8;  // the weight's units (8 columns x 4 rows of a step) a thread: 32 RUNS in all
   __shared__ __attribute__((aligned(16))) char smem[LDS];
   __shared__ float rs_s[BM];
+  __shared__ int32_t rows_s[2 * BM];  // (RoPE) the tile's rows' places, then their cache rows
   float* Cs = (float*)smem;  // [CROWS][BN + 4]: the output tile (after the K loop)
 
   const int64_t M = a.M, ybase = 0;
@@ -537,6 +548,7 @@ __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, i
     } else if (ah == 0) {
       rs_s[ar] = 1.f;
     }
+    if (a.kind == FH_EP_ROPE_KV && ah == 1) stage_rope_rows(a, rows_s, BM, ar, xrow);
   };
   // Each group runs a loop of its own (the same barriers, in the same order), so that the compiler sees one group's
   // loads alone and waits only for the set a store takes, not for the loads issued after it. Step s's operands are
@@ -588,7 +600,8 @@ __global__ __launch_bounds__(2 * GM_THREADS, 1) void gemm_pp_kernel(MatArgs a, i
             Cs[(r0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LDC + wc + 32 * j + (lane & 31)] = acc[i][j][r];
     }
     __syncthreads();
-    gemm_epilogue<CROWS, NT, BN>(a, g, Cs, rs_s + h * CROWS, tn, m0 + h * CROWS, M, ybase, t);
+    gemm_epilogue<CROWS, NT, BN>(a, g, Cs, rs_s + h * CROWS, tn, m0 + h * CROWS, M, ybase, t, rows_s + h * CROWS,
+                                 rows_s + BM + h * CROWS);
     if (h + 1 < BM / CROWS) __syncthreads();  // (the next pass rewrites Cs)
   }
 }
