@@ -175,18 +175,22 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
 
     // S^T for the tile's two blocks of 32 keys: block kb's value r of lane (ql, hh) is key 32 kb + 8 (r / 4) + 4 hh +
     // r % 4, query ql
+    // (the two blocks' products interleaved, a 16-dimension step at a time: two independent MFMAs for each pair of
+    // fragment reads, rather than one block's chain of 8 waiting on each read in turn)
     floatx16 s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
 #pragma unroll
-      for (int st = 0; st < HD / 16; ++st) {
+    for (int st = 0; st < HD / 16; ++st)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
         const bf16x8 kf = *(const bf16x8*)(Ks + (32 * kb + ql) * KLD + 16 * st + 8 * hh);
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kb], 0, 0, 0);
       }
-    }
-    // scale, mask past the query's place (only on a tile reaching past the wave's first row), and the online softmax
+    // mask past the query's place (only on a tile reaching past the wave's first row), and the online softmax: the
+    // max of the raw scores (the scale is positive), and each exponent's scale and shift as one fused multiply-add
     float mt = PA_MASKED;
     if (k0 + PA_BK - 1 > wave_first) {
       const int kq = (int)(qplace - k0);  // (the key's offset in the tile: visible up to this)
@@ -195,7 +199,7 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = 32 * kb + 8 * (r >> 2) + 4 * hh + (r & 3);
-          const float v = key <= kq ? s[kb][r] * scale2 : PA_MASKED;
+          const float v = key <= kq ? s[kb][r] : PA_MASKED;
           s[kb][r] = v;
           mt = fmaxf(mt, v);
         }
@@ -203,20 +207,17 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_kernel(PrefArgs a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s[kb][r] *= scale2;
-          mt = fmaxf(mt, s[kb][r]);
-        }
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mn = fmaxf(m, mt);
+    const float mn = fmaxf(m, mt == PA_MASKED ? PA_MASKED : mt * scale2);
     const float alpha = __builtin_amdgcn_exp2f(m - mn);
     float rsum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(s[kb][r] - mn);
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][r], scale2, -mn));
         s[kb][r] = p;
         rsum += p;
       }
