@@ -281,10 +281,11 @@ def config2_rate(dev, steps=50, warmup=5, place=143):
   nbytes = dec.weight_bytes() + c.layers * 2 * c.kv * dec.hd * (place + 1) * 2
   del dec
   torch.cuda.empty_cache()
-  # the step's launches (embedding; qkv, attention, combine, o, gate_up, down a block; output layer; pick), each
-  # replaced by a one-workgroup read of 4 KiB in a graph of as many launches: what the launches alone cost
+  # the step's launches (embedding; qkv, attention, o, gate_up, down a block, the attention one launch at a context
+  # of at most 4 chunks of 64 rows; output layer; pick), each replaced by a one-workgroup read of 4 KiB in a graph
+  # of as many launches: what the launches alone cost
   from ferrite_amd import lib
-  launches = 6 * c.layers + 3
+  launches = 5 * c.layers + 3
   buf, sink = torch.ones(1024, device=dev), torch.empty(64, dtype=torch.int32, device=dev)
   floor = timed_graph(lambda: [lib.call("fh_read_probe", buf.data_ptr(), 4096, sink.data_ptr(), 1,
                                         torch.cuda.current_stream().cuda_stream) for _ in range(launches)], 5, stream)

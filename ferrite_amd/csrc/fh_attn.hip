@@ -11,7 +11,8 @@
 // workgroup's (p v, max, sum) goes to the workspace, and the second kernel combines the S parts of each (row, head):
 // a thread a part's statistics and a dimension's values, all loaded in one round with the row's place, one exp(max -
 // the largest) a thread. A kernel boundary, not a fence, orders the two: on MI355X an agent-scope release (an L2
-// write-back on each XCD) and a counter cost more than the ~1.4 us boundary. A row reads only the cache rows its
+// write-back on each XCD) and a counter cost more than the ~1.4 us boundary. A row of at most 4 chunks (a short
+// context) is one workgroup's instead (attention_short): a group of waves a chunk, the parts combined in LDS. A row reads only the cache rows its
 // place reaches. A block-float cache (bfp8 or bfp4) is decoded into the same bf16 tiles as it is staged, exactly (a
 // run's values are bf16 values), so its results are bit for bit a bf16 cache's of those values.
 #include <math.h>
@@ -137,14 +138,75 @@ __device__ inline AttArgs cmb_preloaded(const AttArgs& a0, const float* part, co
   return a;
 }
 
+// One chunk's arithmetic for a wave (its query head): the lane's row's score (its keys in LDS dotted with the head's
+// q), the running max and sum of exps (online softmax), and p v into o, a lane dimensions DL lane .. DL lane + DL - 1;
+// n rows of the chunk are the row's. ps: the wave's row of p in LDS.
+template <int HD, int CF>
+__device__ __forceinline__ void chunk_arith(const AttArgs& a, const char* ks, const char* vs, float* ps, const float* qh,
+                                            int lane, int n, float& m, float& l, float (&o)[HD / 64]) {
+  using Loader = ChunkLoader<HD, CF>;
+  constexpr bool BF = CF != FH_F32;
+  constexpr int DL = HD / 64, ES = Loader::ES, V16 = HD * ES / 16, RW = Loader::RW;
+  // the lane's row's score: its keys (from LDS) dotted with the head's q
+  float s2[2] = {0.f, 0.f};
+  const char* krow = ks + lane * RW;
+#pragma unroll
+  for (int p = 0; p < V16; ++p) {
+    const uint4 w4 = *(const uint4*)(krow + 16 * p);
+    const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+    const float4 qa = *(const float4*)(qh + p * (16 / ES)), qb = BF ? *(const float4*)(qh + p * 8 + 4) : qa;
+    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (BF) {
+        s2[0] = fmaf(qv[2 * j], __uint_as_float(w[j] << 16), s2[0]);
+        s2[1] = fmaf(qv[2 * j + 1], __uint_as_float(w[j] & 0xFFFF0000u), s2[1]);
+      } else {
+        s2[j & 1] = fmaf(qv[j], __uint_as_float(w[j]), s2[j & 1]);
+      }
+    }
+  }
+  const bool valid = lane < n;
+  const float sc = valid ? (s2[0] + s2[1]) * a.scale : -INFINITY;
+  const float mn = fmaxf(m, wave_max(sc));   // the running max (finite: the chunk has a row)
+  const float p = valid ? expf(sc - mn) : 0.f;
+  const float f = expf(m - mn);              // (0 on the first chunk)
+  l = fmaf(l, f, wave_sum(p));
+  m = mn;
+  ps[lane] = p;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the wave's p visible to all its lanes
+
+  // p v: a lane dimensions DL lane .. DL lane + DL - 1
+#pragma unroll
+  for (int i = 0; i < DL; ++i) o[i] *= f;
+#pragma unroll 4
+  for (int t4 = 0; t4 < ATT_CHUNK / 4; ++t4) {
+    const float4 p4 = *(const float4*)(ps + 4 * t4);
+    const float pt[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const char* vrw = vs + (4 * t4 + u) * RW + DL * ES * lane;
+      if constexpr (BF && DL == 2) {
+        const uint32_t w = *(const uint32_t*)vrw;
+        o[0] = fmaf(pt[u], __uint_as_float(w << 16), o[0]);
+        o[1] = fmaf(pt[u], __uint_as_float(w & 0xFFFF0000u), o[1]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < DL; ++i) {
+          const float x = BF ? __uint_as_float((uint32_t)((const uint16_t*)vrw)[i] << 16) : ((const float*)vrw)[i];
+          o[i] = fmaf(pt[u], x, o[i]);
+        }
+      }
+    }
+  }
+}
+
 template <int HD, int CF, bool QLDS>
 __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(FH_ATT_PRELOAD, AttArgs a0) {
   const AttArgs a = att_preloaded(a0, pq, pcache, pplaces, pfirst, pcache_len, pmax_chunks, pheads, pkv_heads);
   using Loader = ChunkLoader<HD, CF>;
-  constexpr bool BF = CF != FH_F32;            // the tiles in bf16 (a bf16 or block-float cache)
   constexpr int DL = HD / 64;                  // dimensions a lane (p v, the combine)
-  constexpr int ES = Loader::ES;
-  constexpr int V16 = HD * ES / 16;            // 16-byte pieces a row in LDS
   constexpr int RW = Loader::RW;               // (16 more than the row: a lane's 16-byte reads of its own row spread
                                                // over the banks)
   extern __shared__ __attribute__((aligned(16))) char att_smem[];
@@ -189,59 +251,7 @@ __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(FH_ATT_PRELOAD,
     if (c + S < nchunks)  // the next chunk's first round in flight during this one's arithmetic
       ld.load(a, kr + (int64_t)S * ATT_CHUNK, vr + (int64_t)S * ATT_CHUNK, rows_of(c + S), 0, tid, nthreads);
 
-    // the lane's row's score: its keys (from LDS) dotted with the head's q
-    float s2[2] = {0.f, 0.f};
-    const char* krow = ks + lane * RW;
-#pragma unroll
-    for (int p = 0; p < V16; ++p) {
-      const uint4 w4 = *(const uint4*)(krow + 16 * p);
-      const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
-      const float4 qa = *(const float4*)(qh + p * (16 / ES)), qb = BF ? *(const float4*)(qh + p * 8 + 4) : qa;
-      const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (BF) {
-          s2[0] = fmaf(qv[2 * j], __uint_as_float(w[j] << 16), s2[0]);
-          s2[1] = fmaf(qv[2 * j + 1], __uint_as_float(w[j] & 0xFFFF0000u), s2[1]);
-        } else {
-          s2[j & 1] = fmaf(qv[j], __uint_as_float(w[j]), s2[j & 1]);
-        }
-      }
-    }
-    const bool valid = lane < n;
-    const float sc = valid ? (s2[0] + s2[1]) * a.scale : -INFINITY;
-    const float mn = fmaxf(m, wave_max(sc));   // the running max (finite: the chunk has a row)
-    const float p = valid ? expf(sc - mn) : 0.f;
-    const float f = expf(m - mn);              // (0 on the first chunk)
-    l = fmaf(l, f, wave_sum(p));
-    m = mn;
-    ps[lane] = p;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the wave's p visible to all its lanes
-
-    // p v: a lane dimensions DL lane .. DL lane + DL - 1
-#pragma unroll
-    for (int i = 0; i < DL; ++i) o[i] *= f;
-#pragma unroll 4
-    for (int t4 = 0; t4 < ATT_CHUNK / 4; ++t4) {
-      const float4 p4 = *(const float4*)(ps + 4 * t4);
-      const float pt[4] = {p4.x, p4.y, p4.z, p4.w};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const char* vrw = vs + (4 * t4 + u) * RW + DL * ES * lane;
-        if constexpr (BF && DL == 2) {
-          const uint32_t w = *(const uint32_t*)vrw;
-          o[0] = fmaf(pt[u], __uint_as_float(w << 16), o[0]);
-          o[1] = fmaf(pt[u], __uint_as_float(w & 0xFFFF0000u), o[1]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < DL; ++i) {
-            const float x = BF ? __uint_as_float((uint32_t)((const uint16_t*)vrw)[i] << 16) : ((const float*)vrw)[i];
-            o[i] = fmaf(pt[u], x, o[i]);
-          }
-        }
-      }
-    }
+    chunk_arith<HD, CF>(a, ks, vs, ps, qh, lane, n, m, l, o);
     __syncthreads();  // the tiles and p are rewritten by the next chunk
   }
   if (parts == 1) {  // the row's only part: o itself
@@ -254,6 +264,82 @@ __global__ __launch_bounds__(64 * ATT_REP) void attention_kernel(FH_ATT_PRELOAD,
 #pragma unroll
   for (int i = 0; i < DL; ++i) pp[DL * lane + i] = o[i];
   if (lane == 0) { pp[HD] = m; pp[HD + 1] = l; }
+}
+
+// A short row (at most G chunks, G rep waves at most 16): one workgroup a (key head, batch row) takes the whole row,
+// a group of rep waves a chunk (group g chunk g, in LDS of its own), each the chunk's arithmetic above; the groups'
+// (p v, max, sum) then meet in LDS and group 0's waves write o: no second kernel (its launch is most of a short row's
+// cost). The combine's arithmetic is attention_combine's (each part weighted by exp(its max - the largest)).
+template <int HD, int CF>
+__global__ __launch_bounds__(64 * ATT_REP) void attention_short(FH_ATT_PRELOAD, AttArgs a0) {
+  const AttArgs a = att_preloaded(a0, pq, pcache, pplaces, pfirst, pcache_len, pmax_chunks, pheads, pkv_heads);
+  using Loader = ChunkLoader<HD, CF>;
+  constexpr int DL = HD / 64, RW = Loader::RW;
+  extern __shared__ __attribute__((aligned(16))) char att_smem[];
+  const int kvh = blockIdx.y, b = blockIdx.z;
+  const int rep = a.heads / a.kv_heads;
+  const int tid = threadIdx.x, lane = tid & 63, gthreads = 64 * rep;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = wave / rep, wq = wave - g * rep;  // this wave's chunk and query head of the key head
+  const int gtid = tid - g * gthreads;
+  const int h = kvh * rep + wq;
+  int64_t row0, length;
+  row_range(a, b, row0, length);
+  const int nchunks = (int)((length + ATT_CHUNK - 1) / ATT_CHUNK);  // (at most G: the host's launch)
+  const bool has = g < nchunks;
+  const int64_t rest = length - (int64_t)g * ATT_CHUNK;
+  const int n = has ? (int)(rest < ATT_CHUNK ? rest : ATT_CHUNK) : 0;
+  char* base = att_smem + (size_t)g * (2 * ATT_CHUNK * RW + (size_t)rep * (ATT_CHUNK + HD) * 4);  // the group's
+  char* ks = base;
+  char* vs = base + ATT_CHUNK * RW;
+  float* ps = (float*)(base + 2 * ATT_CHUNK * RW) + wq * ATT_CHUNK;
+  float* qs = (float*)(base + 2 * ATT_CHUNK * RW) + rep * ATT_CHUNK;  // the key head's query heads' q
+  const int64_t kr = (int64_t)kvh * a.cache_len + row0 + (int64_t)g * ATT_CHUNK;
+  const int64_t vr = (int64_t)(a.kv_heads + kvh) * a.cache_len + row0 + (int64_t)g * ATT_CHUNK;
+
+  Loader ld;
+  if (has) {
+    ld.load(a, kr, vr, n, 0, gtid, gthreads);
+    const float* qrow = a.q + ((int64_t)b * a.heads + (int64_t)kvh * rep) * HD;
+    const float4 qp = *(const float4*)(qrow + 4 * min(gtid, rep * HD / 4 - 1));
+    if (gtid < rep * HD / 4) *(float4*)(qs + 4 * gtid) = qp;
+    ld.store(ks, vs, 0, gtid, gthreads);
+    for (int i0 = 4 * gthreads; i0 < Loader::PIECES; i0 += 4 * gthreads) {  // (tiles beyond a round a thread)
+      ld.load(a, kr, vr, n, i0, gtid, gthreads);
+      ld.store(ks, vs, i0, gtid, gthreads);
+    }
+  }
+  __syncthreads();
+  float m = -INFINITY, l = 0.f, o[DL];
+#pragma unroll
+  for (int i = 0; i < DL; ++i) o[i] = 0.f;
+  if (has) chunk_arith<HD, CF>(a, ks, vs, ps, qs + wq * HD, lane, n, m, l, o);
+  __syncthreads();  // (the tiles are free: each wave's part goes where its group's keys were)
+  float* part = (float*)base + wq * (HD + 2);
+  if (has) {
+#pragma unroll
+    for (int i = 0; i < DL; ++i) part[DL * lane + i] = o[i];
+    if (lane == 0) { part[HD] = m; part[HD + 1] = l; }
+  }
+  __syncthreads();
+  if (g != 0) return;
+  const size_t gstride = (2 * ATT_CHUNK * RW + (size_t)rep * (ATT_CHUNK + HD) * 4) / 4;  // (floats between groups)
+  const float* p0 = (const float*)att_smem + wq * (HD + 2);
+  float top = -INFINITY;
+  for (int c = 0; c < nchunks; ++c) top = fmaxf(top, p0[c * gstride + HD]);
+  float den = 0.f, num[DL];
+#pragma unroll
+  for (int i = 0; i < DL; ++i) num[i] = 0.f;
+  for (int c = 0; c < nchunks; ++c) {
+    const float* pc = p0 + c * gstride;
+    const float wc = nchunks == 1 ? 1.f : expf(pc[HD] - top);
+    den = fmaf(wc, pc[HD + 1], den);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) num[i] = fmaf(wc, pc[DL * lane + i], num[i]);
+  }
+  const int64_t ob = (int64_t)h * HD + DL * lane;
+#pragma unroll
+  for (int i = 0; i < DL; ++i) put_o(a, b, ob + i, num[i] / den);
 }
 
 // The same chunk walk on the matrix cores, for a workgroup that takes several chunks (the throughput case: many rows)
@@ -546,6 +632,24 @@ static void launch_attention(int cf, bool q_lds, dim3 grid, dim3 block, size_t l
 }
 
 template <int HD, int CF>
+static void launch_attention_short(dim3 grid, dim3 block, size_t lds, hipStream_t s, const AttArgs& a) {
+  static const hipError_t allowed = hipFuncSetAttribute((const void*)attention_short<HD, CF>,
+      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  (void)allowed;  // (a refusal shows as the launch's error)
+  hipLaunchKernelGGL((attention_short<HD, CF>), grid, block, lds, s, FH_ATT_ARGS(a), a);
+}
+
+template <int HD>
+static void launch_attention_short(int cf, dim3 grid, dim3 block, size_t lds, hipStream_t s, const AttArgs& a) {
+  switch (cf) {
+    case FH_F32: launch_attention_short<HD, FH_F32>(grid, block, lds, s, a); break;
+    case FH_BF16: launch_attention_short<HD, FH_BF16>(grid, block, lds, s, a); break;
+    case FH_BFP8: launch_attention_short<HD, FH_BFP8>(grid, block, lds, s, a); break;
+    default: launch_attention_short<HD, FH_BFP4>(grid, block, lds, s, a); break;
+  }
+}
+
+template <int HD, int CF>
 static void launch_attention_mfma(dim3 grid, dim3 block, hipStream_t s, const AttArgs& a) {
   static const hipError_t allowed = hipFuncSetAttribute((const void*)attention_mfma<HD, CF>,
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)att_mfma_lds(HD));
@@ -676,6 +780,19 @@ extern "C" int fh_attention_decode(const float* q, const void* cache, int cache_
     return (int)std::min<int64_t>(a.max_chunks, std::max<int64_t>(1, (cus * per_cu + pairs - 1) / pairs));
   };
   hipStream_t s = as_stream(stream);
+  // a short context (2-4 chunks): each row in one workgroup, a group of waves a chunk, no combine launch
+  const size_t glds = att_lds(head_dim, es, rep, true);
+  if (a.max_chunks > 1 && a.max_chunks <= 4 && a.max_chunks * rep <= ATT_REP && a.max_chunks * glds <= (size_t)lds_cu) {
+    a.splits = 1;
+    const dim3 grid(1, kv_heads, batch), block(64 * rep * a.max_chunks);
+    const size_t lds = a.max_chunks * glds;
+    switch (head_dim) {
+      case 64: launch_attention_short<64>(cache_dtype, grid, block, lds, s, a); break;
+      case 128: launch_attention_short<128>(cache_dtype, grid, block, lds, s, a); break;
+      default: launch_attention_short<256>(cache_dtype, grid, block, lds, s, a); break;
+    }
+    return check_launch("fh_attention_decode");
+  }
   // the matrix cores where workgroups walk several chunks (many rows: throughput) of a bf16 or block-float cache
   if (cache_dtype != FH_F32 && head_dim <= 128) {
     const int sm = splits_for((int64_t)att_mfma_lds(head_dim), 4);
