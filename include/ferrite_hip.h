@@ -205,7 +205,8 @@ int fh_embed_rows(const void* table, int table_dtype, int64_t vocab, int64_t dim
  * matrix-core matmuls take); heads / kv_heads at most 16. Flash decoding: the keys are shared out among
  * workgroups in chunks of 64 rows of one key head (each cache byte read once, for all the query heads that share it),
  * each writing its partial result and softmax statistics to the workspace, and a second kernel combines the chunks
- * by exp-weights (ferrite/compiler.py:1138-1145); a context of one chunk writes o directly. Scores, softmax and sums
+ * by exp-weights (ferrite/compiler.py:1138-1145); a context of one chunk writes o directly, and one of 2-4 chunks is
+ * one workgroup's a row (a group of waves a chunk, the parts combined in LDS, the workspace unused). Scores, softmax and sums
  * are fp32; where many rows make workgroups walk several chunks of a bf16 or block-float cache, the products run on
  * the matrix cores with q and the softmax weights each as two bf16 terms (within 2^-16 of their fp32 values). The
  * workspace holds no state between calls (what a call does not write, it does not read). */
