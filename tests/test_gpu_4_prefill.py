@@ -78,10 +78,10 @@ def test_attention_prefill_rejects(cuda):
     ops().attention_prefill(torch.zeros(8, 96, device="cuda"), torch.zeros(2, 10, 96, device="cuda"), 1, 1, 96, 0, 0)
 
 
-@pytest.mark.parametrize("dim", [576, 4096, 5000])
+@pytest.mark.parametrize("dim", [576, 4096, 578, 5000])
 def test_rms_rows(cuda, dim):
-  # a row of up to 4096 values held in registers (576: a partial last round of 256; 4096: all 16 rounds full), past
-  # that the row read twice (5000)
+  # a row of up to 4096 values held in registers, 4 a load where the row allows it (576: a partial last round of 1024;
+  # 4096: all 4 rounds full), one a load otherwise (578: not a multiple of 4); past 4096 the row read twice (5000)
   rng = np.random.default_rng(33)
   c = OL.model(dim=dim, eps=1e-5)
   x = rng.normal(0, 3, (37, dim)).astype(np.float32)
