@@ -65,6 +65,23 @@ def test_gemm_shapes(cuda, fmt):
     within(yb, xb @ wv, 2.0 ** -8 * np.abs(xb @ wv) + bound, (M, K, N, "bf16 out"))
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+def test_skinny_row_counts(cuda, fmt):
+  # every row count around the skinny kernel's 16-row blocks (one, two or four a workgroup: 1-16, 17-32, 33-64), a
+  # pass of 64 and a second pass past it (65), with one-run items (N of 3 runs: the last item alone) and pairs of runs
+  rng = np.random.default_rng(21)
+  K = 320
+  for N in (48, 256):
+    w = wide(rng, (K, N)) * 0.02
+    bw = ops().pack(to_gpu(w), fmt)
+    wv = O.bfp(w, fmt)
+    for M in (1, 2, 15, 16, 17, 31, 32, 33, 47, 48, 49, 63, 64, 65):
+      x = rng.normal(0, 1, (M, K)).astype(np.float32)
+      xb = O.bf16(x).astype(np.float64)
+      y = ops().gemm(to_gpu(x, torch.bfloat16), bw).cpu().numpy()
+      within(y, xb @ wv, 1e-5 * (np.abs(xb) @ np.abs(wv)) + 1e-30, (fmt, N, M))
+
+
 def test_gemm_exact_integers(cuda):
   # small integers (exact in bf16) times a power of 2 per run: every product and sum exact in fp32, so bit for bit;
   # and x @ I returns x's bf16 values
