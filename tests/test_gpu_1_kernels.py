@@ -296,6 +296,34 @@ def test_attention_decode(cuda, hd, heads, kv):
   assert np.array_equal(o, o2)
 
 
+@pytest.mark.parametrize("hd,heads,kv", [(64, 9, 3), (128, 32, 8), (128, 8, 2)])
+def test_attention_decode_short_contexts(cuda, hd, heads, kv):
+  # contexts of 2-4 chunks of 64 (a row in one workgroup, a group of waves a chunk, the parts combined in LDS: no
+  # second kernel), rows ending in each chunk and on their edges, against numpy; fp32 and bf16 caches, and bf16 o
+  # bit for bit the fp32 result rounded
+  rng = np.random.default_rng(9 + hd + heads)
+  for context in (65, 128, 129, 192, 256):
+    batch = 5
+    places = np.array([0, 63, 64, context - 2, context - 1], np.int32)
+    first = np.arange(batch, dtype=np.int32) * context
+    cache = rng.normal(0, 1, (2 * kv, batch * context, hd)).astype(np.float32)
+    q = rng.normal(0, 1, (batch, heads * hd)).astype(np.float32)
+    ws = ops().attention_workspace(batch, heads, hd, context)
+    for cd in (torch.float32, torch.bfloat16):
+      cv = cache if cd == torch.float32 else O.bf16(cache)
+      args = (heads, kv, hd, to_gpu(places, torch.int32), to_gpu(first, torch.int32), context, ws)
+      o = ops().attention_decode(to_gpu(q), to_gpu(cache, cd), *args).cpu().numpy()
+      ob = ops().attention_decode(to_gpu(q), to_gpu(cache, cd), *args, o=torch.empty(q.shape, dtype=torch.bfloat16, device="cuda"))
+      assert torch.equal(ob.cpu(), torch.from_numpy(o).to(torch.bfloat16)), (context, cd)
+      for b in range(batch):
+        n = places[b] + 1
+        k = np.repeat(cv[:kv, first[b]:first[b] + n], heads // kv, 0)
+        v = np.repeat(cv[kv:, first[b]:first[b] + n], heads // kv, 0)
+        qq = q[b].reshape(heads, 1, hd).astype(np.float64)
+        want = (OL.softmax(qq @ k.swapaxes(-1, -2) / math.sqrt(hd)) @ v).reshape(-1)
+        assert np.abs(o[b] - want).max() <= 1e-5 * np.abs(want).max() + 1e-6, (context, cd, b)
+
+
 @pytest.mark.parametrize("hd,heads,kv,batch,part", [(128, 32, 8, 16, 1000), (64, 9, 3, 64, 600)])
 def test_attention_decode_many_rows(cuda, hd, heads, kv, batch, part):
   # many rows x key heads: few enough workgroups that each walks several chunks of its row (online softmax across
